@@ -1,0 +1,226 @@
+"""Benchmark of the dense-contraction hot path on one MI355X.
+
+Headline workload: Conv2D forward + dX + dW on
+x [32,64,56,56] U[-1,1), w [64,64,3,3] He-normal, stride 1, padding 1,
+upstream gradient all-ones.  One step = one forward, one backward-data and one
+backward-filter pass (the latter includes its split-K reduce), inputs already
+resident in HBM.  Also reported: matmul 4096 forward + dA + dB (config 2).
+
+Prints ONE JSON line.  Timing uses HIP events recorded on the stream the
+kernels are launched on (torch's current stream, passed to the C ABI).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+METRIC = ("Conv2D fwd+bwd TFLOP/s and % FP32 MFMA peak (N32 C64 56x56 3x3); "
+          "matmul TFLOP/s")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3_resnet")
+    ap.add_argument("--matmul-n", type=int, default=4096)
+    ap.add_argument("--matmul-steps", type=int, default=5)
+    ap.add_argument("--no-matmul", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-images", type=int, default=16,
+                    help="images of the workload timed on the CPU oracle")
+    return ap.parse_args()
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, images, flops_per_image):
+    """The oracle (C restatement of the reference loops, single thread) on a
+    bounded sample of the same workload: `images` of the batch, one forward
+    plus one backward_buffers pass (dX and dW in one visit, as the reference
+    computes them)."""
+    import numpy as np
+
+    from katsu_amd import synth
+    from oracle import oracle as O
+    c = dict(cfg)
+    c["x"] = (images,) + tuple(cfg["x"][1:])
+    x, w = synth.conv_inputs(c)
+    g = np.ones(synth.out_shape(c), np.float32)
+    t0 = time.perf_counter()
+    O.conv2d_forward(x, w, c["stride"], c["pad"])
+    O.conv2d_backward(x, w, g, c["stride"], c["pad"])
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(flops_per_image * images / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{images} of {cfg['x'][0]} images: forward + backward_buffers "
+                   f"(dX and dW in one visit pass), {dt:.2f} s on 1 thread of "
+                   f"{cpu_model()} ({os.cpu_count()} logical CPUs visible)"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one "
+              "GPU (multi-GPU sharding is a design in DESIGN.md, not measured)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from katsu_amd import ops, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    cfg = synth.CONV_CONFIGS[args.workload]
+    st, pad = cfg["stride"], cfg["pad"]
+    x, w = synth.conv_inputs(cfg)
+    yshape = synth.out_shape(cfg)
+    xd = torch.from_numpy(x).to(dev)
+    wd = torch.from_numpy(w).to(dev)
+    gd = torch.ones(yshape, device=dev, dtype=torch.float32)
+    yd = torch.empty(yshape, device=dev, dtype=torch.float32)
+    dxd = torch.empty_like(xd)
+    dwd = torch.empty_like(wd)
+    ws = torch.empty(max(1, ops.bwd_filter_workspace_bytes(x.shape, w.shape, st, pad)),
+                     device=dev, dtype=torch.uint8)
+    pass_flops = synth.conv_flops(cfg)
+    step_flops = 3 * pass_flops
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        ops.conv2d_forward(xd, wd, st, pad, out=yd)
+        if ev is not None:
+            ev[1].record()
+        ops.conv2d_backward_data(gd, wd, x.shape, st, pad, out=dxd)
+        if ev is not None:
+            ev[2].record()
+        ops.conv2d_backward_filter(xd, gd, w.shape, st, pad, out=dwd, workspace=ws)
+        if ev is not None:
+            ev[3].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
+              for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(args.steps):
+        step(events[i])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    per = {"fwd": [], "bwd_data": [], "bwd_filter": []}
+    for ev in events:
+        per["fwd"].append(ev[0].elapsed_time(ev[1]))
+        per["bwd_data"].append(ev[1].elapsed_time(ev[2]))
+        per["bwd_filter"].append(ev[2].elapsed_time(ev[3]))
+    kernels = {}
+    for name, ts in per.items():
+        avg = float(np.mean(ts))
+        kernels[name] = {"avg_us": round(avg * 1e3, 2),
+                         "median_us": round(float(np.median(ts)) * 1e3, 2),
+                         "tflops": round(pass_flops / (avg * 1e-3) / 1e12, 2)}
+    dominant = max(kernels, key=lambda k: kernels[k]["avg_us"])
+    dom_avg_s = kernels[dominant]["avg_us"] * 1e-6
+    achieved = pass_flops / dom_avg_s / 1e12
+    value = step_flops / (ms_per_step * 1e-3) / 1e12
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dominant)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64: x U[-1,1), w He-normal, G all-ones)",
+        "config": {"workload": f"{args.workload}: Conv2D fwd+dX+dW",
+                   "x": list(cfg["x"]), "w": list(cfg["w"]), "stride": st, "padding": pad,
+                   "flop_per_step": step_flops, "parallelism": "none (1 GPU)"},
+        "pct_fp32_mfma_peak": round(100.0 * value / PEAK_FP32_MFMA_TFLOPS, 2),
+        "kernels": kernels,
+        "roofline": {"bound": "mfma", "kernel": dominant,
+                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": traffic},
+    }
+
+    if not args.no_matmul:
+        n = args.matmul_n
+        a = torch.from_numpy(synth.uniform(synth.SEED_X, (n, n))).to(dev)
+        b = torch.from_numpy(synth.uniform(synth.SEED_W, (n, n))).to(dev)
+        g = torch.ones((n, n), device=dev)
+        c = torch.empty((n, n), device=dev)
+        da = torch.zeros_like(a)
+        db = torch.zeros_like(b)
+
+        def mstep():
+            ops.gemm(a, b, n, n, n, out=c)
+            ops.matmul_vjp(a, b, g, da, db)
+
+        mstep()
+        torch.cuda.synchronize()
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(args.matmul_steps):
+            mstep()
+        s1.record()
+        torch.cuda.synchronize()
+        mms = s0.elapsed_time(s1) / args.matmul_steps
+        mflops = 3 * 2 * n ** 3
+        out["matmul"] = {"n": n, "ms_per_step": round(mms, 4),
+                         "tflops": round(mflops / (mms * 1e-3) / 1e12, 3),
+                         "pct_fp32_mfma_peak": round(100 * mflops / (mms * 1e-3) / 1e12
+                                                     / PEAK_FP32_MFMA_TFLOPS, 2)}
+
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
+                                           step_flops / cfg["x"][0])
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,126 @@
+/*
+ * katsu_hip.h -- C ABI of the MI355X (gfx950) dense-contraction path.
+ *
+ * This library replaces the four crate-internal kernel seams of Katsu's
+ * katsu-core (paths relative to the reference repository root):
+ *
+ *   S1  matmul forward     crates/katsu-core/src/tensor.rs:264-273
+ *   S2  matmul VJPs        crates/katsu-core/src/tensor.rs:424-444
+ *   S3  conv forward       crates/katsu-core/src/conv2d.rs:98-103
+ *   S4  conv backward      crates/katsu-core/src/conv2d.rs:284-290
+ *                          (reached from conv2d.rs:127 and tensor.rs:375)
+ *
+ * Layouts are the reference's: row-major matrices, NCHW activations, OIHW
+ * weights, all contiguous f32.  Every entry point returns a katsu_status;
+ * nothing aborts or throws across the ABI.
+ *
+ * Two families of entry points:
+ *   - host-pointer ("drop-in") entry points take the caller's host buffers,
+ *     as the reference's slices are, copy them to the device, run on the
+ *     library's stream and return once the outputs are written back;
+ *   - *_dev entry points take device pointers and a hipStream_t (passed as
+ *     void*, 0 = the null stream) and return right after the launch.
+ *
+ * Threading: the reference engine is single-threaded (Rc handles,
+ * tensor.rs:95-99).  Calls are serialised by an internal mutex, so the
+ * library is safe to call from several threads, but the host-pointer entry
+ * points share one stream and one staging pool.
+ */
+#ifndef KATSU_HIP_H
+#define KATSU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum katsu_status {
+    KATSU_OK = 0,
+    KATSU_E_INVALID = 1,  /* bad argument or shape; nothing was launched */
+    KATSU_E_NODEVICE = 2, /* no HIP device, or device/runtime init failed */
+    KATSU_E_OOM = 3,      /* device allocation failed */
+    KATSU_E_LAUNCH = 4,   /* kernel launch, copy or synchronisation failed */
+} katsu_status;
+
+/* Convolution geometry, the fields of the reference's `struct Geometry`
+ * (conv2d.rs:168-180).  n: batch, c: in channels, h/w: input size,
+ * k: out channels, r/s: kernel height/width, stride/pad: equal on both axes
+ * (conv2d.rs:11-12), oh/ow: output size.  Callers fill n..pad and either
+ * fill oh/ow or call katsu_hip_conv2d_geometry. */
+typedef struct katsu_conv_geom {
+    uint64_t n, c, h, w, k, r, s, stride, pad, oh, ow;
+} katsu_conv_geom;
+
+/* Version string of this library. */
+const char *katsu_hip_version(void);
+
+/* Human-readable text for a katsu_status. */
+const char *katsu_hip_strerror(int status);
+
+/* Selects the first HIP device and creates the library stream.  Called
+ * implicitly by every entry point that needs the device; idempotent. */
+int katsu_hip_init(void);
+
+/* Frees the staging pool and workspace and destroys the stream. */
+void katsu_hip_shutdown(void);
+
+/* Completes *g: checks it the way Geometry::new does (conv2d.rs:183-224:
+ * positive OIHW dims and stride, positive H and W, kernel within the padded
+ * input, no size overflow) and writes oh = (h + 2*pad - r)/stride + 1 and
+ * ow likewise.  Batch 0 is accepted.  Returns KATSU_E_INVALID otherwise. */
+int katsu_hip_conv2d_geometry(katsu_conv_geom *g);
+
+/* ---- S1/S2: matmul ------------------------------------------------------
+ * C[m,n] = beta*C + op(A)[m,k] . op(B)[k,n], beta in {0, 1}.
+ *   op(A) = A   (A stored [m,k]) when trans_a == 0,
+ *           A^T (A stored [k,m]) when trans_a == 1; likewise B.
+ * Tensor::matmul (tensor.rs:264-273) is trans_a=0, trans_b=0, beta=0.
+ * The Matmul VJP (tensor.rs:424-444) is dA += G.B^T (trans_b=1, beta=1)
+ * followed by dB += A^T.G (trans_a=1, beta=1), in that order, because the
+ * two pending buffers are the same buffer when A and B are the same node.
+ * With beta == 0, C is not read.  k == 0 writes beta*C (tensor.rs:265,421).
+ */
+int katsu_hip_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n,
+                       size_t k, int trans_a, int trans_b, float beta);
+int katsu_hip_gemm_f32_dev(const float *a, const float *b, float *c, size_t m, size_t n,
+                           size_t k, int trans_a, int trans_b, float beta, void *stream);
+
+/* ---- S3: convolution forward --------------------------------------------
+ * y[n,k,oh,ow] = sum over valid (c,r,s) of x[n,c,oy*stride+r-pad,
+ * ox*stride+s-pad] * w[k,c,r,s]  (Conv2D::forward, conv2d.rs:95-115;
+ * cross-correlation, padded taps contribute nothing).  y is overwritten. */
+int katsu_hip_conv2d_fwd_f32(const float *x, const float *w, float *y,
+                             const katsu_conv_geom *g);
+int katsu_hip_conv2d_fwd_f32_dev(const float *x, const float *w, float *y,
+                                 const katsu_conv_geom *g, void *stream);
+
+/* ---- S4: convolution backward (backward_buffers, conv2d.rs:269-292) -----
+ * dx = beta*dx + d(sum(gy*y))/dx:   dx[x] += gy[y] * w[w] over the visit.
+ * beta = 0 reproduces the fresh buffer of conv2d.rs:284; beta = 1 adds into
+ * an engine's pending buffer (tensor.rs:383-390). */
+int katsu_hip_conv2d_bwd_data_f32(const float *gy, const float *w, float *dx,
+                                  const katsu_conv_geom *g, float beta);
+int katsu_hip_conv2d_bwd_data_f32_dev(const float *gy, const float *w, float *dx,
+                                      const katsu_conv_geom *g, float beta, void *stream);
+
+/* dw = beta*dw + sum over the visit of gy[y] * x[x]  (conv2d.rs:289).
+ * The reduction over n*oh*ow is split across workgroups and reduced in a
+ * fixed order, so results are deterministic run to run.
+ * The _dev form needs `workspace` of katsu_hip_conv2d_bwd_filter_workspace
+ * bytes (device memory, 256-byte aligned); pass NULL to use a library-owned
+ * buffer, which is allocated (hipMalloc) on first need and kept. */
+int katsu_hip_conv2d_bwd_filter_workspace(const katsu_conv_geom *g, size_t *bytes);
+int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,
+                                    const katsu_conv_geom *g, float beta);
+int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *dw,
+                                        const katsu_conv_geom *g, float beta,
+                                        void *workspace, size_t workspace_bytes,
+                                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KATSU_HIP_H */

@@ -1,0 +1,689 @@
+// katsu_hip.hip -- C ABI (include/katsu_hip.h) over the gfx950 MFMA engine.
+//
+// Replaces the reference's kernel seams (paths relative to the reference
+// repository root):
+//   katsu_hip_gemm_f32*                 tensor.rs:264-273 (fwd), 424-444 (VJPs)
+//   katsu_hip_conv2d_fwd_f32*           conv2d.rs:98-103
+//   katsu_hip_conv2d_bwd_data_f32*      conv2d.rs:288 (dx half of backward_buffers)
+//   katsu_hip_conv2d_bwd_filter_f32*    conv2d.rs:289 (dw half of backward_buffers)
+//   katsu_hip_conv2d_geometry           conv2d.rs:183-224 (Geometry::new checks)
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/katsu_hip.h"
+#include "igemm.hpp"
+
+namespace katsu {
+namespace {
+
+constexpr int64_t kI32Max = 0x7fffffff;
+
+// ---------------------------------------------------------------------------
+// Small helper kernels.
+
+// out = beta * out, used when a reduction is empty (k == 0 or batch == 0).
+__global__ void __launch_bounds__(256) scale_kernel(float *p, int64_t n, float beta) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+        p[i] = (beta == 0.f) ? 0.f : beta * p[i];
+}
+
+// dw = beta*dw + sum_s ws[s][e], s ascending: a fixed order, so the result is
+// the same on every run.
+__global__ void __launch_bounds__(256) dw_reduce_kernel(const float *__restrict__ ws,
+                                                        float *__restrict__ dw, int64_t elems,
+                                                        int splits, float beta) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= elems) return;
+    float acc = 0.f;
+    for (int s = 0; s < splits; ++s) acc += ws[(int64_t)s * elems + e];
+    dw[e] = (beta == 0.f) ? acc : beta * dw[e] + acc;
+}
+
+// ---------------------------------------------------------------------------
+// Library state.
+
+struct Buffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct State {
+    std::mutex mu;
+    bool ready = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    Buffer staging[4];
+    Buffer workspace;
+};
+
+State &state() {
+    static State s;
+    return s;
+}
+
+int map_hip(hipError_t e) {
+    if (e == hipSuccess) return KATSU_OK;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return KATSU_E_OOM;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) return KATSU_E_NODEVICE;
+    return KATSU_E_LAUNCH;
+}
+
+int init_locked(State &s) {
+    if (s.ready) return KATSU_OK;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return KATSU_E_NODEVICE;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return KATSU_E_NODEVICE;
+    if (hipSetDevice(dev) != hipSuccess) return KATSU_E_NODEVICE;
+    // Default priority, non-blocking with respect to the null stream.
+    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess)
+        return KATSU_E_NODEVICE;
+    s.device = dev;
+    s.ready = true;
+    return KATSU_OK;
+}
+
+int ensure(Buffer &b, size_t bytes) {
+    if (b.bytes >= bytes) return KATSU_OK;
+    if (b.ptr) {
+        (void)hipFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    size_t want = std::max<size_t>(bytes, 256);
+    hipError_t e = hipMalloc(&b.ptr, want);
+    if (e != hipSuccess) {
+        b.ptr = nullptr;
+        return map_hip(e);
+    }
+    b.bytes = want;
+    return KATSU_OK;
+}
+
+int launch_status() { return map_hip(hipGetLastError()); }
+
+int launch_scale(float *p, int64_t n, float beta, hipStream_t st) {
+    if (n <= 0 || beta == 1.f) return KATSU_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+    scale_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(p, n, beta);
+    return launch_status();
+}
+
+bool beta_ok(float beta) { return beta == 0.f || beta == 1.f; }
+
+// ---------------------------------------------------------------------------
+// Tile configurations.  BM spans the output's "row" dimension (oc, c, or m),
+// BN the contiguous one (pixels, or n).
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+};
+using CfgS = Cfg<16, 256, 16, 16, 64>;   // rows <= 16 (tiny channel counts)
+using CfgM = Cfg<64, 128, 16, 32, 64>;   // rows <= 64
+using CfgL = Cfg<128, 128, 16, 64, 64>;  // large
+using CfgW = Cfg<64, 64, 32, 32, 32>;    // dW: oc x (c,r,s), long split reductions
+
+template <class C, class Prob>
+int run(const Prob &p, int64_t blocks, hipStream_t st) {
+    if (blocks <= 0) return KATSU_OK;
+    if (blocks > kI32Max) return KATSU_E_INVALID;
+    igemm_kernel<C::BM, C::BN, C::BK, C::WM, C::WN, Prob>
+        <<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(p);
+    return launch_status();
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// GEMM.
+
+template <class C, bool A_KM, bool B_KM>
+int gemm_cfg(const float *a, int64_t a_si, int64_t a_sk, const float *b, int64_t b_si,
+             int64_t b_sk, float *c, int64_t m, int64_t n, int64_t k, float beta,
+             hipStream_t st) {
+    GemmProb<A_KM, B_KM> p;
+    p.a = {a, a_si, a_sk, (int)m};
+    p.b = {b, b_si, b_sk, (int)n};
+    p.c = {c, n, (int)m, (int)n, beta};
+    p.K = (int)k;
+    p.tiles_m = (int)cdiv(m, C::BM);
+    p.tiles_n = (int)cdiv(n, C::BN);
+    p.group = 8;
+    return run<C>(p, (int64_t)p.tiles_m * p.tiles_n, st);
+}
+
+template <class C>
+int gemm_dispatch(const float *a, const float *b, float *c, int64_t m, int64_t n, int64_t k,
+                  int ta, int tb, float beta, hipStream_t st) {
+    // op(A)[i][kk]: A stored [m][k] -> (si=k, sk=1), contiguous along k (IMAJOR);
+    //               A stored [k][m] -> (si=1, sk=m), contiguous along i (KMAJOR).
+    // op(B)[kk][j]: B stored [k][n] -> (si=1, sk=n), KMAJOR;
+    //               B stored [n][k] -> (si=k, sk=1), IMAJOR.
+    if (!ta && !tb) return gemm_cfg<C, false, true>(a, k, 1, b, 1, n, c, m, n, k, beta, st);
+    if (!ta && tb) return gemm_cfg<C, false, false>(a, k, 1, b, k, 1, c, m, n, k, beta, st);
+    if (ta && !tb) return gemm_cfg<C, true, true>(a, 1, m, b, 1, n, c, m, n, k, beta, st);
+    return gemm_cfg<C, true, false>(a, 1, m, b, k, 1, c, m, n, k, beta, st);
+}
+
+int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_t k, int ta,
+             int tb, float beta, hipStream_t st) {
+    if (!beta_ok(beta) || (ta != 0 && ta != 1) || (tb != 0 && tb != 1)) return KATSU_E_INVALID;
+    if ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max)
+        return KATSU_E_INVALID;
+    if (m == 0 || n == 0) return KATSU_OK;
+    if (!c) return KATSU_E_INVALID;
+    if (k == 0) return launch_scale(c, (int64_t)m * (int64_t)n, beta, st);
+    if (!a || !b) return KATSU_E_INVALID;
+    if (m >= 128 && n >= 128)
+        return gemm_dispatch<CfgL>(a, b, c, m, n, k, ta, tb, beta, st);
+    if (m <= 16) return gemm_dispatch<CfgS>(a, b, c, m, n, k, ta, tb, beta, st);
+    return gemm_dispatch<CfgM>(a, b, c, m, n, k, ta, tb, beta, st);
+}
+
+// ---------------------------------------------------------------------------
+// Convolution geometry (the checks of Geometry::new, conv2d.rs:183-224, plus
+// the 32-bit index limits of the kernels).
+
+bool mul_ok(uint64_t a, uint64_t b, uint64_t *out) { return !__builtin_mul_overflow(a, b, out); }
+
+int geometry_fill(katsu_conv_geom *g) {
+    if (!g) return KATSU_E_INVALID;
+    if (g->c == 0 || g->k == 0 || g->r == 0 || g->s == 0 || g->stride == 0)
+        return KATSU_E_INVALID;  // validate_weights, conv2d.rs:156-166
+    if (g->h == 0 || g->w == 0) return KATSU_E_INVALID;  // conv2d.rs:190
+    uint64_t pad2;
+    if (!mul_ok(g->pad, 2, &pad2)) return KATSU_E_INVALID;
+    uint64_t ph, pw;
+    if (__builtin_add_overflow(g->h, pad2, &ph) || __builtin_add_overflow(g->w, pad2, &pw))
+        return KATSU_E_INVALID;
+    if (ph < g->r || pw < g->s) return KATSU_E_INVALID;  // kernel exceeds padded input
+    g->oh = (ph - g->r) / g->stride + 1;
+    g->ow = (pw - g->s) / g->stride + 1;
+    return KATSU_OK;
+}
+
+// Checked problem sizes used by the launchers.
+struct ConvDims {
+    int N, C, H, W, K, R, S, st, pad, OH, OW;
+    int HW, CHW, OHW, KOHW, RS, CRS;
+    int64_t npix_out, npix_in;  // N*OH*OW, N*H*W
+};
+
+int conv_dims(const katsu_conv_geom *g, ConvDims *d) {
+    if (!g) return KATSU_E_INVALID;
+    katsu_conv_geom t = *g;
+    if (geometry_fill(&t) != KATSU_OK) return KATSU_E_INVALID;
+    if (t.oh != g->oh || t.ow != g->ow) return KATSU_E_INVALID;
+    // Per-image and per-filter element counts must fit the kernels' 32-bit
+    // index math; so must the pixel counts that index GEMM columns.
+    uint64_t hw, chw, ohw, kohw, rs, crs, kcrs, npo, npi;
+    if (!mul_ok(t.h, t.w, &hw) || !mul_ok(hw, t.c, &chw) || !mul_ok(t.oh, t.ow, &ohw) ||
+        !mul_ok(ohw, t.k, &kohw) || !mul_ok(t.r, t.s, &rs) || !mul_ok(rs, t.c, &crs) ||
+        !mul_ok(crs, t.k, &kcrs) || !mul_ok(ohw, t.n, &npo) || !mul_ok(hw, t.n, &npi))
+        return KATSU_E_INVALID;
+    const uint64_t lim = (uint64_t)kI32Max;
+    if (chw > lim || kohw > lim || kcrs > lim || npo > lim || npi > lim || t.pad > lim ||
+        t.stride > lim || t.h + 2 * t.pad > lim || t.w + 2 * t.pad > lim)
+        return KATSU_E_INVALID;
+    d->N = (int)t.n;
+    d->C = (int)t.c;
+    d->H = (int)t.h;
+    d->W = (int)t.w;
+    d->K = (int)t.k;
+    d->R = (int)t.r;
+    d->S = (int)t.s;
+    d->st = (int)t.stride;
+    d->pad = (int)t.pad;
+    d->OH = (int)t.oh;
+    d->OW = (int)t.ow;
+    d->HW = (int)hw;
+    d->CHW = (int)chw;
+    d->OHW = (int)ohw;
+    d->KOHW = (int)kohw;
+    d->RS = (int)rs;
+    d->CRS = (int)crs;
+    d->npix_out = (int64_t)npo;
+    d->npix_in = (int64_t)npi;
+    return KATSU_OK;
+}
+
+FastDiv fdiv(int64_t d) { return make_fastdiv((uint32_t)std::max<int64_t>(1, d)); }
+
+// ---------------------------------------------------------------------------
+// Forward.
+
+template <class C>
+int fwd_cfg(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
+    FwdProb p;
+    p.a = {w, d.CRS, 1, d.K};
+    FwdColView &b = p.b;
+    b.x = x;
+    b.H = d.H;
+    b.W = d.W;
+    b.HW = d.HW;
+    b.S = d.S;
+    b.RS = d.RS;
+    b.OW = d.OW;
+    b.OHW = d.OHW;
+    b.npix = (int)d.npix_out;
+    b.stride = d.st;
+    b.pad = d.pad;
+    b.chw = d.CHW;
+    b.fd_ohw = fdiv(d.OHW);
+    b.fd_ow = fdiv(d.OW);
+    b.fd_rs = fdiv(d.RS);
+    b.fd_s = fdiv(d.S);
+    p.c = {y, d.K, d.OHW, (int)d.npix_out, (int64_t)d.KOHW, fdiv(d.OHW)};
+    p.CRS = d.CRS;
+    p.tiles_m = (int)cdiv(d.K, C::BM);
+    const int64_t tiles_n = cdiv(d.npix_out, C::BN);
+    return run<C>(p, tiles_n * p.tiles_m, st);
+}
+
+int conv_fwd_dev(const float *x, const float *w, float *y, const katsu_conv_geom *g,
+                 hipStream_t st) {
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    if (d.npix_out == 0) return KATSU_OK;
+    if (!x || !w || !y) return KATSU_E_INVALID;
+    if (d.K <= 16) return fwd_cfg<CfgS>(x, w, y, d, st);
+    if (d.K <= 64) return fwd_cfg<CfgM>(x, w, y, d, st);
+    return fwd_cfg<CfgL>(x, w, y, d, st);
+}
+
+// ---------------------------------------------------------------------------
+// Backward data.
+
+template <class C>
+int dx_cfg(const float *gy, const float *w, float *dx, const ConvDims &d, float beta,
+           hipStream_t st) {
+    DxProb p;
+    std::memset(&p, 0, sizeof(p));
+    DxWView &a = p.a;
+    a.w = w;
+    a.C = d.C;
+    a.RS = d.RS;
+    a.S = d.S;
+    a.CRS = d.CRS;
+    a.stride = d.st;
+    DxColView &b = p.b;
+    b.g = gy;
+    b.OH = d.OH;
+    b.OW = d.OW;
+    b.OHW = d.OHW;
+    b.kohw = d.KOHW;
+    DxEpi &e = p.c;
+    e.dx = dx;
+    e.C = d.C;
+    e.HW = d.HW;
+    e.W = d.W;
+    e.stride = d.st;
+    e.chw = d.CHW;
+    e.beta = beta;
+    p.tiles_m = (int)cdiv(d.C, C::BM);
+
+    // Enumerate the stride phases; launch at most kMaxPhases per kernel.
+    const int st2 = d.st * d.st;
+    int rc = KATSU_OK;
+    int64_t tiles = 0;
+    p.nphases = 0;
+    for (int q = 0; q < st2 && rc == KATSU_OK; ++q) {
+        const int py = q / d.st, px = q % d.st;
+        DxPhase P;
+        P.py = py;
+        P.px = px;
+        P.Ha = py < d.H ? (d.H - py + d.st - 1) / d.st : 0;
+        P.Wa = px < d.W ? (d.W - px + d.st - 1) / d.st : 0;
+        P.r0 = (int)(((int64_t)py + d.pad) % d.st);
+        P.s0 = (int)(((int64_t)px + d.pad) % d.st);
+        P.dy = (int)(((int64_t)py + d.pad - P.r0) / d.st);
+        P.dx = (int)(((int64_t)px + d.pad - P.s0) / d.st);
+        P.Ru = P.r0 < d.R ? (d.R - P.r0 + d.st - 1) / d.st : 0;
+        P.Su = P.s0 < d.S ? (d.S - P.s0 + d.st - 1) / d.st : 0;
+        const int64_t npix = (int64_t)d.N * P.Ha * P.Wa;
+        if (npix == 0) continue;
+        P.npix = (int)npix;
+        P.kred = d.K * P.Ru * P.Su;
+        P.tiles_n = (int)cdiv(npix, C::BN);
+        P.fd_hawa = fdiv((int64_t)P.Ha * P.Wa);
+        P.fd_wa = fdiv(P.Wa);
+        P.fd_rusu = fdiv((int64_t)P.Ru * P.Su);
+        P.fd_su = fdiv(P.Su);
+        P.tile_begin = (int)tiles;
+        p.ph[p.nphases++] = P;
+        tiles += (int64_t)P.tiles_n * p.tiles_m;
+        if (tiles > kI32Max) return KATSU_E_INVALID;
+        if (p.nphases == kMaxPhases || q == st2 - 1) {
+            rc = run<C>(p, tiles, st);
+            p.nphases = 0;
+            tiles = 0;
+        }
+    }
+    if (rc == KATSU_OK && p.nphases > 0) rc = run<C>(p, tiles, st);
+    return rc;
+}
+
+int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_conv_geom *g,
+                      float beta, hipStream_t st) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    if (d.npix_in == 0) return KATSU_OK;
+    if (!gy || !w || !dx) return KATSU_E_INVALID;
+    if (d.C <= 16) return dx_cfg<CfgS>(gy, w, dx, d, beta, st);
+    if (d.C <= 64) return dx_cfg<CfgM>(gy, w, dx, d, beta, st);
+    return dx_cfg<CfgL>(gy, w, dx, d, beta, st);
+}
+
+// ---------------------------------------------------------------------------
+// Backward filter.
+
+struct DwPlan {
+    int tiles_m, tiles_n, splits, kchunk;
+    size_t ws_bytes;
+};
+
+template <class C>
+DwPlan dw_plan(const ConvDims &d) {
+    DwPlan pl;
+    pl.tiles_m = (int)cdiv(d.K, C::BM);
+    pl.tiles_n = (int)cdiv(d.CRS, C::BN);
+    const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
+    const int64_t npix = d.npix_out;
+    // Aim for ~4 workgroups per CU (256 CUs) but keep every split at least
+    // 8 k-tiles long so the partial traffic stays small next to the GEMM.
+    const int64_t target = 1024;
+    int64_t splits = std::max<int64_t>(1, cdiv(target, tiles));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, npix / (8 * C::BK)));
+    int64_t kchunk = cdiv(cdiv(npix, splits), C::BK) * C::BK;
+    if (kchunk <= 0) kchunk = C::BK;
+    splits = std::max<int64_t>(1, cdiv(npix, kchunk));
+    pl.splits = (int)splits;
+    pl.kchunk = (int)kchunk;
+    pl.ws_bytes = splits > 1 ? (size_t)splits * (size_t)d.K * (size_t)d.CRS * sizeof(float) : 0;
+    return pl;
+}
+
+DwPlan dw_plan_any(const ConvDims &d) { return dw_plan<CfgW>(d); }
+
+template <class C>
+int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float beta,
+           float *ws, hipStream_t st) {
+    const DwPlan pl = dw_plan<C>(d);
+    DwProb p;
+    DwGView &a = p.a;
+    a.g = gy;
+    a.K = d.K;
+    a.OHW = d.OHW;
+    a.kohw = d.KOHW;
+    a.fd_ohw = fdiv(d.OHW);
+    DwColView &b = p.b;
+    b.x = x;
+    b.H = d.H;
+    b.W = d.W;
+    b.HW = d.HW;
+    b.S = d.S;
+    b.RS = d.RS;
+    b.CRS = d.CRS;
+    b.OW = d.OW;
+    b.OHW = d.OHW;
+    b.stride = d.st;
+    b.pad = d.pad;
+    b.chw = d.CHW;
+    b.fd_rs = fdiv(d.RS);
+    b.fd_s = fdiv(d.S);
+    b.fd_ohw = fdiv(d.OHW);
+    b.fd_ow = fdiv(d.OW);
+    const bool direct = pl.splits == 1;
+    p.c.out = direct ? dw : ws;
+    p.c.K = d.K;
+    p.c.CRS = d.CRS;
+    p.c.split_stride = direct ? 0 : (int64_t)d.K * d.CRS;
+    p.c.beta = direct ? beta : 0.f;
+    p.c.split = 0;
+    p.tiles_m = pl.tiles_m;
+    p.tiles_n = pl.tiles_n;
+    p.splits = pl.splits;
+    p.kchunk = pl.kchunk;
+    p.npix = (int)d.npix_out;
+    int rc = run<C>(p, (int64_t)pl.tiles_m * pl.tiles_n * pl.splits, st);
+    if (rc != KATSU_OK || direct) return rc;
+    const int64_t elems = (int64_t)d.K * d.CRS;
+    dw_reduce_kernel<<<dim3((unsigned)cdiv(elems, 256)), dim3(256), 0, st>>>(ws, dw, elems,
+                                                                             pl.splits, beta);
+    return launch_status();
+}
+
+int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_conv_geom *g,
+                        float beta, void *ws, size_t ws_bytes, hipStream_t st,
+                        Buffer *fallback) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    if (!dw) return KATSU_E_INVALID;
+    if (d.npix_out == 0) return launch_scale(dw, (int64_t)d.K * d.CRS, beta, st);
+    if (!x || !gy) return KATSU_E_INVALID;
+    const DwPlan pl = dw_plan_any(d);
+    float *wsp = (float *)ws;
+    if (pl.ws_bytes > 0) {
+        if (!wsp) {
+            if (!fallback) return KATSU_E_INVALID;
+            int rc = ensure(*fallback, pl.ws_bytes);
+            if (rc != KATSU_OK) return rc;
+            wsp = (float *)fallback->ptr;
+        } else if (ws_bytes < pl.ws_bytes) {
+            return KATSU_E_INVALID;
+        }
+    }
+    return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
+}
+
+// ---------------------------------------------------------------------------
+// Host-pointer wrappers: stage through the pool, run, copy back, synchronise.
+
+int h2d(Buffer &b, const float *src, size_t count, hipStream_t st) {
+    const size_t bytes = count * sizeof(float);
+    int rc = ensure(b, bytes);
+    if (rc != KATSU_OK) return rc;
+    if (bytes == 0) return KATSU_OK;
+    return map_hip(hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, st));
+}
+
+int d2h_sync(float *dst, const Buffer &b, size_t count, hipStream_t st) {
+    const size_t bytes = count * sizeof(float);
+    if (bytes) {
+        int rc = map_hip(hipMemcpyAsync(dst, b.ptr, bytes, hipMemcpyDeviceToHost, st));
+        if (rc != KATSU_OK) return rc;
+    }
+    return map_hip(hipStreamSynchronize(st));
+}
+
+}  // namespace
+}  // namespace katsu
+
+using namespace katsu;
+
+extern "C" {
+
+const char *katsu_hip_version(void) { return "katsu-mi355x 0.1.0 (gfx950, fp32 MFMA)"; }
+
+const char *katsu_hip_strerror(int status) {
+    switch (status) {
+        case KATSU_OK: return "ok";
+        case KATSU_E_INVALID: return "invalid argument or shape";
+        case KATSU_E_NODEVICE: return "no HIP device available";
+        case KATSU_E_OOM: return "device allocation failed";
+        case KATSU_E_LAUNCH: return "kernel launch, copy or synchronisation failed";
+        default: return "unknown katsu status";
+    }
+}
+
+int katsu_hip_init(void) {
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return init_locked(s);
+}
+
+void katsu_hip_shutdown(void) {
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (!s.ready) return;
+    (void)hipStreamSynchronize(s.stream);
+    for (Buffer &b : s.staging) {
+        if (b.ptr) (void)hipFree(b.ptr);
+        b = Buffer{};
+    }
+    if (s.workspace.ptr) (void)hipFree(s.workspace.ptr);
+    s.workspace = Buffer{};
+    (void)hipStreamDestroy(s.stream);
+    s.stream = nullptr;
+    s.ready = false;
+}
+
+int katsu_hip_conv2d_geometry(katsu_conv_geom *g) { return geometry_fill(g); }
+
+int katsu_hip_gemm_f32_dev(const float *a, const float *b, float *c, size_t m, size_t n,
+                           size_t k, int trans_a, int trans_b, float beta, void *stream) {
+    return gemm_dev(a, b, c, m, n, k, trans_a, trans_b, beta, (hipStream_t)stream);
+}
+
+int katsu_hip_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                       int trans_a, int trans_b, float beta) {
+    if (!beta_ok(beta) || (trans_a != 0 && trans_a != 1) || (trans_b != 0 && trans_b != 1))
+        return KATSU_E_INVALID;
+    if (m == 0 || n == 0) return KATSU_OK;
+    if (!c || (k > 0 && (!a || !b))) return KATSU_E_INVALID;
+    size_t mn, mk, kn;
+    if (!mul_ok(m, n, (uint64_t *)&mn) || !mul_ok(m, k, (uint64_t *)&mk) ||
+        !mul_ok(k, n, (uint64_t *)&kn))
+        return KATSU_E_INVALID;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    if (k > 0) {
+        if ((rc = h2d(s.staging[0], a, mk, s.stream))) return rc;
+        if ((rc = h2d(s.staging[1], b, kn, s.stream))) return rc;
+    }
+    if (beta != 0.f) {
+        if ((rc = h2d(s.staging[2], c, mn, s.stream))) return rc;
+    } else if ((rc = ensure(s.staging[2], mn * sizeof(float)))) {
+        return rc;
+    }
+    rc = gemm_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
+                  (float *)s.staging[2].ptr, m, n, k, trans_a, trans_b, beta, s.stream);
+    if (rc) return rc;
+    return d2h_sync(c, s.staging[2], mn, s.stream);
+}
+
+int katsu_hip_conv2d_fwd_f32_dev(const float *x, const float *w, float *y,
+                                 const katsu_conv_geom *g, void *stream) {
+    return conv_fwd_dev(x, w, y, g, (hipStream_t)stream);
+}
+
+int katsu_hip_conv2d_fwd_f32(const float *x, const float *w, float *y,
+                             const katsu_conv_geom *g) {
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    const size_t nx = (size_t)d.npix_in * d.C, nw = (size_t)d.K * d.CRS,
+                 ny = (size_t)d.npix_out * d.K;
+    if (ny == 0) return KATSU_OK;
+    if (!x || !w || !y) return KATSU_E_INVALID;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    if ((rc = h2d(s.staging[0], x, nx, s.stream))) return rc;
+    if ((rc = h2d(s.staging[1], w, nw, s.stream))) return rc;
+    if ((rc = ensure(s.staging[2], ny * sizeof(float)))) return rc;
+    rc = conv_fwd_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
+                      (float *)s.staging[2].ptr, g, s.stream);
+    if (rc) return rc;
+    return d2h_sync(y, s.staging[2], ny, s.stream);
+}
+
+int katsu_hip_conv2d_bwd_data_f32_dev(const float *gy, const float *w, float *dx,
+                                      const katsu_conv_geom *g, float beta, void *stream) {
+    return conv_bwd_data_dev(gy, w, dx, g, beta, (hipStream_t)stream);
+}
+
+int katsu_hip_conv2d_bwd_data_f32(const float *gy, const float *w, float *dx,
+                                  const katsu_conv_geom *g, float beta) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    const size_t nx = (size_t)d.npix_in * d.C, nw = (size_t)d.K * d.CRS,
+                 ny = (size_t)d.npix_out * d.K;
+    if (nx == 0) return KATSU_OK;
+    if (!gy || !w || !dx) return KATSU_E_INVALID;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    if ((rc = h2d(s.staging[0], gy, ny, s.stream))) return rc;
+    if ((rc = h2d(s.staging[1], w, nw, s.stream))) return rc;
+    if (beta != 0.f) {
+        if ((rc = h2d(s.staging[2], dx, nx, s.stream))) return rc;
+    } else if ((rc = ensure(s.staging[2], nx * sizeof(float)))) {
+        return rc;
+    }
+    rc = conv_bwd_data_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
+                           (float *)s.staging[2].ptr, g, beta, s.stream);
+    if (rc) return rc;
+    return d2h_sync(dx, s.staging[2], nx, s.stream);
+}
+
+int katsu_hip_conv2d_bwd_filter_workspace(const katsu_conv_geom *g, size_t *bytes) {
+    if (!bytes) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    *bytes = d.npix_out == 0 ? 0 : dw_plan_any(d).ws_bytes;
+    return KATSU_OK;
+}
+
+int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *dw,
+                                        const katsu_conv_geom *g, float beta, void *workspace,
+                                        size_t workspace_bytes, void *stream) {
+    State &s = state();
+    if (workspace) {
+        return conv_bwd_filter_dev(x, gy, dw, g, beta, workspace, workspace_bytes,
+                                   (hipStream_t)stream, nullptr);
+    }
+    std::lock_guard<std::mutex> lock(s.mu);
+    return conv_bwd_filter_dev(x, gy, dw, g, beta, nullptr, 0, (hipStream_t)stream,
+                               &s.workspace);
+}
+
+int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,
+                                    const katsu_conv_geom *g, float beta) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    const size_t nx = (size_t)d.npix_in * d.C, nw = (size_t)d.K * d.CRS,
+                 ny = (size_t)d.npix_out * d.K;
+    if (!dw) return KATSU_E_INVALID;
+    if (ny > 0 && (!x || !gy)) return KATSU_E_INVALID;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    if ((rc = h2d(s.staging[0], x, nx, s.stream))) return rc;
+    if ((rc = h2d(s.staging[1], gy, ny, s.stream))) return rc;
+    if (beta != 0.f) {
+        if ((rc = h2d(s.staging[2], dw, nw, s.stream))) return rc;
+    } else if ((rc = ensure(s.staging[2], nw * sizeof(float)))) {
+        return rc;
+    }
+    rc = conv_bwd_filter_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
+                             (float *)s.staging[2].ptr, g, beta, nullptr, 0, s.stream,
+                             &s.workspace);
+    if (rc) return rc;
+    return d2h_sync(dw, s.staging[2], nw, s.stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+"""Device-tensor entry points over the C ABI (the ``*_dev`` functions).
+
+torch is plumbing here: it owns device memory and the stream.  Every call
+launches the gfx950 kernels of libkatsu_hip.so on torch's current stream;
+nothing is computed by torch.  Host (numpy) entry points live in
+``katsu_amd.host``.
+"""
+import ctypes
+
+import torch
+
+from ._abi import check, geometry, lib
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None and t.numel() else ctypes.c_void_p(0)
+
+
+def _dev_f32(*ts):
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("katsu_amd.ops expects contiguous float32 device tensors")
+
+
+def conv_geom(xshape, wshape, stride, pad):
+    n, c, h, w = xshape
+    k, c2, r, s = wshape
+    if c != c2:
+        raise ValueError("input channels must match weights")
+    return geometry(n, c, h, w, k, r, s, stride, pad)
+
+
+def conv2d_forward(x, w, stride, pad, out=None):
+    """y = conv(x, w): Conv2D::forward (conv2d.rs:95-115)."""
+    _dev_f32(x, w, out)
+    g = conv_geom(x.shape, w.shape, stride, pad)
+    if out is None:
+        out = torch.empty((g.n, g.k, g.oh, g.ow), device=x.device, dtype=torch.float32)
+    check(lib().katsu_hip_conv2d_fwd_f32_dev(_p(x), _p(w), _p(out), ctypes.byref(g), _stream()),
+          "conv2d_fwd")
+    return out
+
+
+def conv2d_backward_data(gy, w, xshape, stride, pad, out=None, beta=0.0):
+    """dx (conv2d.rs:288); beta=1 accumulates into `out`."""
+    _dev_f32(gy, w, out)
+    g = conv_geom(xshape, w.shape, stride, pad)
+    if out is None:
+        out = torch.empty(tuple(xshape), device=gy.device, dtype=torch.float32)
+    check(lib().katsu_hip_conv2d_bwd_data_f32_dev(_p(gy), _p(w), _p(out), ctypes.byref(g),
+                                                   float(beta), _stream()), "conv2d_bwd_data")
+    return out
+
+
+def bwd_filter_workspace_bytes(xshape, wshape, stride, pad):
+    g = conv_geom(xshape, wshape, stride, pad)
+    nbytes = ctypes.c_size_t(0)
+    check(lib().katsu_hip_conv2d_bwd_filter_workspace(ctypes.byref(g), ctypes.byref(nbytes)),
+          "bwd_filter_workspace")
+    return nbytes.value
+
+
+def conv2d_backward_filter(x, gy, wshape, stride, pad, out=None, beta=0.0, workspace=None):
+    """dw (conv2d.rs:289); beta=1 accumulates into `out`.
+
+    `workspace` is an optional uint8/float device tensor of at least
+    bwd_filter_workspace_bytes(); without it the library's own buffer is used."""
+    _dev_f32(x, gy, out)
+    g = conv_geom(x.shape, wshape, stride, pad)
+    if out is None:
+        out = torch.empty(tuple(wshape), device=x.device, dtype=torch.float32)
+    ws = ctypes.c_void_p(workspace.data_ptr()) if workspace is not None else ctypes.c_void_p(0)
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib().katsu_hip_conv2d_bwd_filter_f32_dev(_p(x), _p(gy), _p(out), ctypes.byref(g),
+                                                     float(beta), ws, wsb, _stream()),
+          "conv2d_bwd_filter")
+    return out
+
+
+def gemm(a, b, m, n, k, trans_a=False, trans_b=False, out=None, beta=0.0):
+    """out[m,n] = beta*out + op(a) op(b) (tensor.rs:264-273, 424-444)."""
+    _dev_f32(a, b, out)
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=torch.float32)
+    check(lib().katsu_hip_gemm_f32_dev(_p(a), _p(b), _p(out), m, n, k, int(trans_a),
+                                       int(trans_b), float(beta), _stream()), "gemm")
+    return out
+
+
+def matmul(a, b):
+    """Tensor::matmul forward: [m,k] @ [k,n] (tensor.rs:249-280)."""
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError("matmul inner dimensions differ")
+    return gemm(a, b, m, n, k)
+
+
+def matmul_vjp(a, b, g, da, db):
+    """Matmul VJP (tensor.rs:418-445): da += g b^T, then db += a^T g.
+
+    da and db may be the same tensor (A and B the same node); the two
+    launches run in order on one stream, as the reference's loops do."""
+    m, k = a.shape
+    n = b.shape[1]
+    if m * n == 0 or k == 0:
+        return da, db
+    gemm(g, b, m, k, n, trans_b=True, out=da, beta=1.0)
+    gemm(a, g, k, n, m, trans_a=True, out=db, beta=1.0)
+    return da, db
