@@ -1,0 +1,505 @@
+// direct.hpp -- direct (halo-tile) convolution kernels for gfx950.
+//
+// These kernels cover the convolution passes whose input rows fit an LDS
+// halo tile.  Unlike the generic implicit-GEMM engine (igemm.hpp), which
+// gathers every im2col element with its own index arithmetic, a block here
+// stages whole input rows once -- a [channels][rows][64*CC] tile with the
+// zero padding materialised in LDS -- and every one of the R*S taps reads
+// that tile at a per-lane offset computed once per block plus a tap offset.
+// The tile geometry (row pitch 64*CC, ROWS rows per channel) is a template
+// parameter, so every tap, channel and pipeline-stage offset is an LDS
+// instruction immediate: the MFMA loop is LDS reads and MFMAs only.
+//
+//   direct_fwd_kernel   out[n][co][p] = sum_{ci,r,s} in[n][ci][tap(p,r,s)] * w'(co,ci,r,s)
+//                       forward (WMODE 0: w' = w) and, for stride 1, the
+//                       data gradient (WMODE 1: in = G, w' = w transposed
+//                       and flipped)
+//   direct_dw_kernel    dw partials over a range of output pixels
+//   dw_split_reduce     fixed-order sum of the dw partials
+//
+// MFMA v_mfma_f32_16x16x4_f32 lane layout (wave64), as in igemm.hpp:
+//   A: lane l holds A[i = l%16][k = l/16]; B: lane l holds B[k = l/16][j = l%16]
+//   D: lane l, register v holds D[i = 4*(l/16) + v][j = l%16]
+#pragma once
+
+#include "igemm.hpp"
+
+namespace katsu {
+
+// ---------------------------------------------------------------------------
+// Forward / data-gradient kernel.
+//
+// GEMM view per block: i = output channel (KT of them), j = output pixel
+// (a contiguous range of one image), k = (input channel, tap).  Waves split
+// the KT channels into 16-row slices and the pixel range into WPX parts of
+// F fragments of 16 pixels each.  Input channels are consumed CB at a time
+// through a two-stage LDS pipeline.
+struct DirectArgs {
+    const float *in;   // [N][CI][H][W]
+    const float *w;    // layer weights: WMODE 0 w[CO][CI][R][S]; WMODE 1 w[CI][CO][R][S]
+    float *out;        // [N][CO][OH][OW]
+    int N, CI, H, W, CO, OH, OW, st, pady, padx;
+    int OHW, HW;
+    int64_t in_img, out_img;  // CI*H*W, CO*OH*OW
+    int tile_px;       // output pixels per tile (one image)
+    int tiles_img;     // tiles per image
+    int co_blocks;     // ceil(CO / KT)
+    int ncols;         // halo columns: (OW-1)*st + S  (<= 64*CC)
+    float beta;        // out = beta*out + result (beta in {0, 1})
+    FastDiv fd_ow;     // division by OW
+};
+
+// LDS layout (floats) of the forward kernel.
+template <int KT, int CB, int R, int S, int ROWS, int CC, int WMODE>
+struct DirectFwdGeo {
+    static constexpr int RS = R * S;
+    static constexpr int PITCH = 64 * CC;               // halo row pitch
+    static constexpr int CPITCH = ROWS * PITCH + 16;    // channel pitch, == 16 (mod 32)
+    static constexpr int XS = CB * CPITCH;              // input tile
+    // Weight tile, kept in the global order of its rows:
+    //   WMODE 0: KT rows (co) of CB*RS floats, pitch CB*RS + 1
+    //   WMODE 1: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
+    static constexpr int WROWS = WMODE == 0 ? KT : CB;
+    static constexpr int WLEN = WMODE == 0 ? CB * RS : KT * RS;
+    static constexpr int WPITCH = WMODE == 0 ? WLEN + 1 : WLEN + ((16 - WLEN % 32) + 32) % 32;
+    static constexpr int WS = WROWS * WPITCH;
+    static constexpr int STAGE = XS + WS;
+    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+};
+
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+__global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
+    using Geo = DirectFwdGeo<KT, CB, R, S, ROWS, CC, WMODE>;
+    constexpr int RS = R * S;
+    constexpr int WOC = KT / 16;            // waves along output channels
+    constexpr int TPR = 256 / Geo::WROWS;   // threads per weight row
+    constexpr int WPT = (Geo::WLEN + TPR - 1) / TPR;  // weight floats per thread
+    constexpr int CPW = CB / 4;             // input channels staged per wave
+    static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
+    static_assert(CB % 4 == 0 && 256 % Geo::WROWS == 0, "CB must be a multiple of 4");
+
+    extern __shared__ float smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int woc = wave % WOC, wpx = wave / WOC;
+
+    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int cob = t % a.co_blocks;
+    const int rest = t / a.co_blocks;
+    const int n = rest / a.tiles_img;
+    const int p0 = (rest - n * a.tiles_img) * a.tile_px;
+    const int p1 = min(p0 + a.tile_px, a.OHW);
+    const int oy0 = a.fd_ow.div(p0);
+    const int iy0 = oy0 * a.st - a.pady;
+    const int co0 = cob * KT;
+
+    // Per-lane LDS offset of each fragment's pixel, channel group l/16 folded in.
+    int pix[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        int p = p0 + (wpx * F + f) * 16 + (lane & 15);
+        p = p < p1 ? p : p0;
+        const int oy = a.fd_ow.div(p);
+        const int ox = p - oy * a.OW;
+        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * Geo::PITCH + ox * a.st;
+    }
+    // Per-lane A-fragment base: row co = woc*16 + l%16, channel l/16.
+    const int abase = WMODE == 0
+        ? (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS
+        : (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS;
+
+    // ---- staging: input halo rows ------------------------------------------
+    // Wave w stages channels w + 4j (j < CPW), every row, 64 columns per chunk.
+    const float *inb = a.in + (int64_t)n * a.in_img;
+    bool colok[CC];
+    int colx[CC];
+#pragma unroll
+    for (int c = 0; c < CC; ++c) {
+        const int col = c * 64 + lane;
+        colx[c] = col - a.padx;
+        colok[c] = col < a.ncols && (unsigned)colx[c] < (unsigned)a.W;
+    }
+    float xr[CPW][ROWS][CC];
+
+    // ---- staging: weights ----------------------------------------------------
+    const int wrow = tid / TPR, wcol = tid % TPR;
+    float wr[WPT];
+
+    auto load = [&](int ci0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+            const int ci = ci0 + wave + 4 * j;
+            const bool cok = ci < a.CI;
+            const float *src = inb + (int64_t)ci * a.HW;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const int iy = iy0 + r;
+                const bool rok = cok && (unsigned)iy < (unsigned)a.H;
+#pragma unroll
+                for (int c = 0; c < CC; ++c)
+                    xr[j][r][c] = (rok && colok[c]) ? src[iy * a.W + colx[c]] : 0.f;
+            }
+        }
+        if (WMODE == 0) {
+            // row co = co0 + wrow: CB*RS contiguous floats from w[co][ci0][0][0].
+            const int co = co0 + wrow;
+            const int lim = co < a.CO ? min(CB, a.CI - ci0) * RS : 0;
+            const float *src = a.w + ((int64_t)co * a.CI + ci0) * RS;
+#pragma unroll
+            for (int q = 0; q < WPT; ++q) {
+                const int e = wcol + TPR * q;
+                wr[q] = (e < lim && e < Geo::WLEN) ? src[e] : 0.f;
+            }
+        } else {
+            // row ci = ci0 + wrow: KT*RS contiguous floats from w[ci][co0][0][0].
+            const int ci = ci0 + wrow;
+            const int lim = ci < a.CI ? min(KT, a.CO - co0) * RS : 0;
+            const float *src = a.w + ((int64_t)ci * a.CO + co0) * RS;
+#pragma unroll
+            for (int q = 0; q < WPT; ++q) {
+                const int e = wcol + TPR * q;
+                wr[q] = (e < lim && e < Geo::WLEN) ? src[e] : 0.f;
+            }
+        }
+    };
+
+    auto store = [&](float *base) __attribute__((always_inline)) {
+        float *xs = base + wave * Geo::CPITCH + lane;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int c = 0; c < CC; ++c)
+                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
+        float *ws = base + Geo::XS + wrow * Geo::WPITCH + wcol;
+#pragma unroll
+        for (int q = 0; q < WPT; ++q)
+            if (wcol + TPR * q < Geo::WLEN) ws[TPR * q] = wr[q];
+    };
+
+    floatx4 acc[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) acc[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One k-step kk = (channel quad cs, tap): the A fragment and the F B
+    // fragments it multiplies.  All offsets are compile-time after unrolling.
+    auto fetch = [&](const float *base, const int kk, float (&b)[F], float &av) {
+        const int cs = kk / RS, tap = kk % RS;
+        const int r = tap / S, s = tap % S;
+        const float *ws = base + Geo::XS + abase;
+        av = WMODE == 0 ? ws[cs * 4 * RS + tap] : ws[cs * 4 * Geo::WPITCH + (RS - 1 - tap)];
+        const int toff = cs * 4 * Geo::CPITCH + r * Geo::PITCH + s;
+#pragma unroll
+        for (int f = 0; f < F; ++f) b[f] = base[pix[f] + toff];
+    };
+    auto mma = [&](const float (&b)[F], const float av) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[f], acc[f], 0, 0, 0);
+    };
+    // Software pipeline over the k-steps of one stage: the fragments of step
+    // kk+1 are read while step kk's MFMAs run.  The scheduling barriers keep
+    // the compiler from hoisting every read of the stage (register blow-up).
+    auto compute = [&](const float *base) __attribute__((always_inline)) {
+        constexpr int NK = (CB / 4) * RS;
+        float b0[F], b1[F];
+        float a0, a1;
+        fetch(base, 0, b0, a0);
+#pragma unroll
+        for (int kk = 0; kk < NK; kk += 2) {
+            if (kk + 1 < NK) fetch(base, kk + 1, b1, a1);
+            mma(b0, a0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 2 < NK) fetch(base, kk + 2, b0, a0);
+            if (kk + 1 < NK) mma(b1, a1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Two-stage pipeline: while chunk ch is consumed from one stage, chunk
+    // ch+1 is fetched into registers and written to the other stage.  The
+    // loop is unrolled by two so each stage's base is a constant.
+    const int nch = (a.CI + CB - 1) / CB;
+    float *st0 = smem;
+    float *st1 = smem + Geo::STAGE;
+    load(0);
+    store(st0);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ch += 2) {
+        if (ch + 1 < nch) load((ch + 1) * CB);
+        compute(st0);
+        if (ch + 1 < nch) store(st1);
+        __syncthreads();
+        if (ch + 1 >= nch) break;
+        if (ch + 2 < nch) load((ch + 2) * CB);
+        compute(st1);
+        if (ch + 2 < nch) store(st0);
+        __syncthreads();
+    }
+
+    float *outb = a.out + (int64_t)n * a.out_img;
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const int p = p0 + (wpx * F + f) * 16 + (lane & 15);
+        if (p >= p1) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int co = co0 + woc * 16 + 4 * (lane >> 4) + v;
+            if (co < a.CO) store_beta(outb + (int64_t)co * a.OHW + p, acc[f][v], a.beta);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Filter-gradient kernel.
+//
+// GEMM view: i = output channel (KT per block), j = input channel (CT per
+// block), k = output pixel; one accumulator tile per tap.  A block walks a
+// range of pixel tiles (its split of the reduction), staging G[KT][tile] and
+// the X halo [CT][ROWS][64*CC] for each tile through a two-stage LDS
+// pipeline, and writes one partial dw[KT][CT][R][S] at the end.  Waves split
+// KT x CT into 16 x 16 slices.
+struct DirectDwArgs {
+    const float *x;    // [N][C][H][W]
+    const float *g;    // [N][K][OH][OW]
+    float *out;        // partials [split][K][C*R*S], or dw itself when splits == 1
+    int N, C, H, W, K, OH, OW, st, pad;
+    int OHW, HW, CRS;
+    int64_t x_img, g_img;
+    int tile_px, tiles_img, tiles_total, tiles_per_split;
+    int k_blocks, c_blocks;
+    int ncols;
+    int64_t split_stride;  // floats between partials, or 0 when writing dw directly
+    float beta;            // applied only when writing dw directly
+    FastDiv fd_ow, fd_tiles_img;
+};
+
+template <int KT, int CT, int ROWS, int CC, int GPC>
+struct DirectDwGeo {
+    static constexpr int PITCH = 64 * CC;
+    static constexpr int CPITCH = ROWS * PITCH + 2;   // == 2 (mod 32)
+    static constexpr int GPITCH = 64 * GPC + 2;       // == 2 (mod 32)
+    static constexpr int GS = KT * GPITCH;
+    static constexpr int STAGE = GS + CT * CPITCH;
+    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+};
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
+__global__ void __launch_bounds__(256) direct_dw_kernel(const DirectDwArgs a) {
+    using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
+    constexpr int RS = R * S;
+    constexpr int WK = KT / 16;         // waves along output channels
+    constexpr int CPW = CT / 4;         // input channels staged per wave
+    constexpr int GRW = KT / 4;         // G rows staged per wave
+    static_assert(KT % 16 == 0 && CT % 16 == 0 && (KT / 16) * (CT / 16) == 4,
+                  "4 waves of 16x16 slices");
+
+    extern __shared__ float smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wk = wave % WK, wc = wave / WK;
+
+    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int kb = t % a.k_blocks;
+    const int rest = t / a.k_blocks;
+    const int cb = rest % a.c_blocks;
+    const int split = rest / a.c_blocks;
+    const int k0 = kb * KT, c0 = cb * CT;
+    const int tb = split * a.tiles_per_split;
+    const int te = min(tb + a.tiles_per_split, a.tiles_total);
+
+    bool colok[CC];
+    int colx[CC];
+#pragma unroll
+    for (int c = 0; c < CC; ++c) {
+        const int col = c * 64 + lane;
+        colx[c] = col - a.pad;
+        colok[c] = col < a.ncols && (unsigned)colx[c] < (unsigned)a.W;
+    }
+    float xr[CPW][ROWS][CC];
+    float gr[GRW][GPC];
+
+    struct TileGeo { int n, p0, np, oy0; };
+    auto geo = [&](int tile) __attribute__((always_inline)) {
+        TileGeo tg;
+        tg.n = a.fd_tiles_img.div(tile);
+        tg.p0 = (tile - tg.n * a.tiles_img) * a.tile_px;
+        tg.np = min(a.tile_px, a.OHW - tg.p0);
+        tg.oy0 = a.fd_ow.div(tg.p0);
+        return tg;
+    };
+
+    auto load = [&](const TileGeo &tg) __attribute__((always_inline)) {
+        const float *xb = a.x + (int64_t)tg.n * a.x_img;
+        const float *gb = a.g + (int64_t)tg.n * a.g_img + tg.p0;
+        const int iy0 = tg.oy0 * a.st - a.pad;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+            const int ci = c0 + wave + 4 * j;
+            const bool cok = ci < a.C;
+            const float *src = xb + (int64_t)ci * a.HW;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const int iy = iy0 + r;
+                const bool rok = cok && (unsigned)iy < (unsigned)a.H;
+#pragma unroll
+                for (int c = 0; c < CC; ++c)
+                    xr[j][r][c] = (rok && colok[c]) ? src[iy * a.W + colx[c]] : 0.f;
+            }
+        }
+        // G rows k0 + wave + 4i, pixels lane + 64c of the tile.
+#pragma unroll
+        for (int i = 0; i < GRW; ++i) {
+            const int k = k0 + wave + 4 * i;
+            const bool kok = k < a.K;
+            const float *src = gb + (int64_t)k * a.OHW;
+#pragma unroll
+            for (int c = 0; c < GPC; ++c) {
+                const int px = c * 64 + lane;
+                gr[i][c] = (kok && px < tg.np) ? src[px] : 0.f;
+            }
+        }
+    };
+
+    auto store = [&](float *base) __attribute__((always_inline)) {
+        float *gs = base + wave * Geo::GPITCH + lane;
+#pragma unroll
+        for (int i = 0; i < GRW; ++i)
+#pragma unroll
+            for (int c = 0; c < GPC; ++c) gs[4 * i * Geo::GPITCH + c * 64] = gr[i][c];
+        float *xs = base + Geo::GS + wave * Geo::CPITCH + lane;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int c = 0; c < CC; ++c)
+                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
+    };
+
+    floatx4 acc[RS];
+#pragma unroll
+    for (int i = 0; i < RS; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int arow = (wk * 16 + (lane & 15)) * Geo::GPITCH + (lane >> 4);
+    const int bch = Geo::GS + (wc * 16 + (lane & 15)) * Geo::CPITCH;
+
+    // One k-step covers pixels q0..q0+3 of the tile; lanes beyond the tile
+    // contribute exact zeros (both operands zeroed).
+    auto compute = [&](const float *base, const TileGeo &tg) __attribute__((always_inline)) {
+        for (int q0 = 0; q0 < tg.np; q0 += 4) {
+            const int q = q0 + (lane >> 4);
+            const bool ok = q < tg.np;
+            const int p = tg.p0 + (ok ? q : 0);
+            const int oy = a.fd_ow.div(p);
+            const int ox = p - oy * a.OW;
+            const float *xs = base + bch + (oy - tg.oy0) * a.st * Geo::PITCH + ox * a.st;
+            const float ag = base[arow + q0];
+            const float av = ok ? ag : 0.f;
+#pragma unroll
+            for (int tap = 0; tap < RS; ++tap) {
+                const int r = tap / S, s = tap % S;
+                const float bx = xs[r * Geo::PITCH + s];
+                const float bv = ok ? bx : 0.f;
+                acc[tap] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[tap], 0, 0, 0);
+            }
+        }
+    };
+
+    if (tb < te) {
+        float *st0 = smem;
+        float *st1 = smem + Geo::STAGE;
+        TileGeo cur = geo(tb);
+        load(cur);
+        store(st0);
+        __syncthreads();
+        for (int tile = tb; tile < te; tile += 2) {
+            TileGeo nxt = cur;
+            if (tile + 1 < te) {
+                nxt = geo(tile + 1);
+                load(nxt);
+            }
+            compute(st0, cur);
+            if (tile + 1 < te) store(st1);
+            __syncthreads();
+            if (tile + 1 >= te) break;
+            cur = nxt;
+            if (tile + 2 < te) {
+                nxt = geo(tile + 2);
+                load(nxt);
+            }
+            compute(st1, cur);
+            if (tile + 2 < te) store(st0);
+            __syncthreads();
+            cur = nxt;
+        }
+    }
+
+    // D[i = oc][j = c] per tap -> out[split][oc][c][tap].
+    float *ob = a.out + (int64_t)split * a.split_stride;
+    const int c = c0 + wc * 16 + (lane & 15);
+    if (c < a.C) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int k = k0 + wk * 16 + 4 * (lane >> 4) + v;
+            if (k >= a.K) continue;
+            float *dst = ob + (int64_t)k * a.CRS + c * RS;
+#pragma unroll
+            for (int tap = 0; tap < RS; ++tap) {
+                if (a.split_stride == 0)
+                    store_beta(dst + tap, acc[tap][v], a.beta);
+                else
+                    dst[tap] = acc[tap][v];
+            }
+        }
+    }
+}
+
+// dw[e] = beta*dw[e] + sum_s part[s][e].  Thread (e4, grp) sums splits
+// grp, grp+G, ... in order for four consecutive elements; the G group sums
+// are then added in group order.  The summation tree is fixed by (splits,
+// G), so the result is identical on every run.  Partial rows are pstride
+// floats apart (pstride % 4 == 0, so the float4 loads stay aligned).
+template <int G>
+__global__ void __launch_bounds__(256) dw_split_reduce(const float *__restrict__ part,
+                                                       float *__restrict__ dw, int64_t elems,
+                                                       int64_t pstride, int splits, float beta) {
+    constexpr int E4 = 256 / G;  // float4 columns per block
+    __shared__ float4 red[G][E4];
+    const int col = threadIdx.x % E4, grp = threadIdx.x / E4;
+    const int64_t e = ((int64_t)blockIdx.x * E4 + col) * 4;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e + 3 < elems) {
+        for (int k = grp; k < splits; k += G) {
+            const float4 v = *reinterpret_cast<const float4 *>(part + (int64_t)k * pstride + e);
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+    } else if (e < elems) {
+        for (int k = grp; k < splits; k += G) {
+            const float *pk = part + (int64_t)k * pstride + e;
+            s.x += pk[0];
+            if (e + 1 < elems) s.y += pk[1];
+            if (e + 2 < elems) s.z += pk[2];
+        }
+    }
+    red[grp][col] = s;
+    __syncthreads();
+    if (grp != 0 || e >= elems) return;
+    float4 tot = red[0][col];
+#pragma unroll
+    for (int q = 1; q < G; ++q) {
+        const float4 v = red[q][col];
+        tot.x += v.x;
+        tot.y += v.y;
+        tot.z += v.z;
+        tot.w += v.w;
+    }
+    const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
+    for (int i = 0; i < 4 && e + i < elems; ++i) store_beta(dw + e + i, tv[i], beta);
+}
+
+}  // namespace katsu

@@ -16,6 +16,7 @@
 
 #include "../../include/katsu_hip.h"
 #include "igemm.hpp"
+#include "direct.hpp"
 
 namespace katsu {
 namespace {
@@ -255,6 +256,241 @@ int conv_dims(const katsu_conv_geom *g, ConvDims *d) {
 FastDiv fdiv(int64_t d) { return make_fastdiv((uint32_t)std::max<int64_t>(1, d)); }
 
 // ---------------------------------------------------------------------------
+// Direct (halo-tile) kernels: planning and launch.  A planner returns false
+// when its kernel variant does not fit the problem (kernel size, halo
+// columns or rows, LDS, too few blocks to fill the chip); the caller then
+// tries the next variant and finally the implicit-GEMM engine, which takes
+// every shape.
+
+constexpr size_t kLdsMax = 163840;         // bytes of LDS a gfx950 workgroup may use
+constexpr int64_t kMinDirectBlocks = 256;  // one per CU at least
+
+// Rows of output touched by any tile of `tile_px` consecutive pixels.
+int64_t tile_row_span(int64_t tile_px, int64_t OW, int64_t OH) {
+    int64_t span;
+    if (tile_px % OW == 0) span = tile_px / OW;
+    else if (OW % tile_px == 0) span = 1;
+    else span = (tile_px + OW - 2) / OW + 1;
+    return std::min(span, OH);
+}
+
+// Dynamic LDS above 64 KiB must be opted into once per kernel.
+template <class K>
+int lds_optin(K kernel, size_t bytes) {
+    if (bytes <= 65536) return KATSU_OK;
+    static bool done = false;  // one flag per kernel instantiation
+    if (!done) {
+        if (hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)bytes) != hipSuccess)
+            return KATSU_E_LAUNCH;
+        done = true;
+    }
+    return KATSU_OK;
+}
+
+// A "forward-shaped" problem: out[n][co] = sum_ci,taps in[n][ci] * w'.
+struct DirectFwdProblem {
+    const float *in, *w;
+    float *out;
+    int64_t N, CI, H, W, CO, R, S, st, pady, padx, OH, OW;
+    float beta;
+};
+
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    using Geo = DirectFwdGeo<KT, CB, R, S, ROWS, CC, WMODE>;
+    if (P.R != R || P.S != S) return false;
+    static_assert(Geo::kBytes <= kLdsMax, "LDS");
+    constexpr int WPX = 4 / (KT / 16);
+    const int64_t OHW = P.OH * P.OW;
+    const int64_t ncols = (P.OW - 1) * P.st + S;
+    if (ncols > 64 * CC) return false;
+    const int64_t co_blocks = cdiv(P.CO, KT);
+    const int64_t tpmax = (int64_t)WPX * F * 16;
+    // The fewest tiles that fit, but enough blocks to fill the chip.
+    int64_t tiles_img = std::max(cdiv(OHW, tpmax), cdiv(kMinDirectBlocks, co_blocks * P.N));
+    for (int attempt = 0; attempt < 64; ++attempt, ++tiles_img) {
+        const int64_t tile_px = cdiv(OHW, tiles_img);
+        if (2 * tile_px < tpmax) return false;  // fragments would be under half full
+        const int64_t ntiles = cdiv(OHW, tile_px);
+        const int64_t rows_max = (tile_row_span(tile_px, P.OW, P.OH) - 1) * P.st + R;
+        if (rows_max > ROWS) continue;
+        const int64_t blocks = co_blocks * P.N * ntiles;
+        if (blocks < kMinDirectBlocks || blocks > kI32Max) return false;
+        DirectArgs a;
+        a.in = P.in;
+        a.w = P.w;
+        a.out = P.out;
+        a.N = (int)P.N;
+        a.CI = (int)P.CI;
+        a.H = (int)P.H;
+        a.W = (int)P.W;
+        a.CO = (int)P.CO;
+        a.OH = (int)P.OH;
+        a.OW = (int)P.OW;
+        a.st = (int)P.st;
+        a.pady = (int)P.pady;
+        a.padx = (int)P.padx;
+        a.OHW = (int)OHW;
+        a.HW = (int)(P.H * P.W);
+        a.in_img = P.CI * P.H * P.W;
+        a.out_img = P.CO * OHW;
+        a.tile_px = (int)tile_px;
+        a.tiles_img = (int)ntiles;
+        a.co_blocks = (int)co_blocks;
+        a.ncols = (int)ncols;
+        a.beta = P.beta;
+        a.fd_ow = fdiv(P.OW);
+        auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE>;
+        if ((*rc = lds_optin(kern, Geo::kBytes)) != KATSU_OK) return true;
+        kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
+        *rc = launch_status();
+        return true;
+    }
+    return false;
+}
+
+// Forward variants in order of preference; false = none applies.
+template <int WMODE>
+bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    if (P.CO >= 64 && direct_fwd_launch<64, 13, 8, 3, 3, 7, 1, WMODE>(P, st, rc)) return true;
+    return false;
+}
+
+// Filter gradient.  Plan first (the workspace size is part of the API), then launch.
+struct DirectDwPlan {
+    bool ok = false;
+    int variant = -1;
+    DirectDwArgs a;
+    int64_t blocks = 0;
+    int splits = 0;
+    int64_t pstride = 0;  // floats between partials
+    size_t ws_bytes = 0;
+};
+
+constexpr int64_t kDwTargetBlocks = 512;
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
+bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
+    using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
+    static_assert(Geo::kBytes <= kLdsMax, "LDS");
+    if (d.R != R || d.S != S) return false;
+    const int64_t tmax = 64 * GPC;
+    const int64_t OHW = d.OHW;
+    const int64_t ncols = (int64_t)(d.OW - 1) * d.st + S;
+    if (ncols > 64 * CC) return false;
+    // Whole output rows per tile when they fit, else a divisor of the row.
+    int64_t tile_px = 0;
+    if (d.OW <= tmax) {
+        tile_px = (int64_t)d.OW * (tmax / d.OW);
+    } else {
+        for (int64_t t = tmax; t >= 16; --t)
+            if (d.OW % t == 0) {
+                tile_px = t;
+                break;
+            }
+        if (tile_px == 0) tile_px = tmax;
+    }
+    tile_px = std::min<int64_t>(tile_px, OHW);
+    // Fewer rows per tile until the halo fits ROWS.
+    while (tile_px > d.OW && (tile_row_span(tile_px, d.OW, d.OH) - 1) * d.st + R > ROWS)
+        tile_px -= d.OW;
+    if ((tile_row_span(tile_px, d.OW, d.OH) - 1) * d.st + R > ROWS) return false;
+    const int64_t tiles_img = cdiv(OHW, tile_px);
+    const int64_t tiles_total = (int64_t)d.N * tiles_img;
+    const int64_t kb = cdiv(d.K, KT), cb = cdiv(d.C, CT);
+    int64_t splits = std::max<int64_t>(1, cdiv(kDwTargetBlocks, kb * cb));
+    splits = std::min(splits, tiles_total);
+    const int64_t tps = cdiv(tiles_total, splits);
+    splits = cdiv(tiles_total, tps);
+    const int64_t blocks = kb * cb * splits;
+    if (blocks < kMinDirectBlocks / 2 || blocks > kI32Max) return false;
+    const int64_t elems = (int64_t)d.K * d.CRS;
+    DirectDwArgs &a = pl->a;
+    a.x = nullptr;
+    a.g = nullptr;
+    a.out = nullptr;
+    a.N = d.N;
+    a.C = d.C;
+    a.H = d.H;
+    a.W = d.W;
+    a.K = d.K;
+    a.OH = d.OH;
+    a.OW = d.OW;
+    a.st = d.st;
+    a.pad = d.pad;
+    a.OHW = d.OHW;
+    a.HW = d.HW;
+    a.CRS = d.CRS;
+    a.x_img = d.CHW;
+    a.g_img = d.KOHW;
+    a.tile_px = (int)tile_px;
+    a.tiles_img = (int)tiles_img;
+    a.tiles_total = (int)tiles_total;
+    a.tiles_per_split = (int)tps;
+    a.k_blocks = (int)kb;
+    a.c_blocks = (int)cb;
+    a.ncols = (int)ncols;
+    a.split_stride = 0;
+    a.beta = 0.f;
+    a.fd_ow = fdiv(d.OW);
+    a.fd_tiles_img = fdiv(tiles_img);
+    pl->ok = true;
+    pl->blocks = blocks;
+    pl->splits = (int)splits;
+    pl->pstride = (elems + 3) / 4 * 4;
+    pl->ws_bytes = splits > 1 ? (size_t)splits * (size_t)pl->pstride * sizeof(float) : 0;
+    return true;
+}
+
+// Variant table: the planner and the kernel of each direct dW variant.
+#define KATSU_DW_VARIANTS(X) X(0, 64, 16, 3, 3, 3, 1, 1)
+
+DirectDwPlan direct_dw_plan_any(const ConvDims &d) {
+    DirectDwPlan pl;
+#define KATSU_DW_TRY(id, KT, CT, R, S, ROWS, CC, GPC)                                  \
+    if (pl.variant < 0 && d.K >= KT && direct_dw_plan<KT, CT, R, S, ROWS, CC, GPC>(d, &pl)) \
+        pl.variant = id;
+    KATSU_DW_VARIANTS(KATSU_DW_TRY)
+#undef KATSU_DW_TRY
+    pl.ok = pl.variant >= 0;
+    return pl;
+}
+
+int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw, float beta,
+                     float *ws, hipStream_t st) {
+    DirectDwArgs &a = pl.a;
+    const bool direct = pl.splits == 1;
+    a.x = x;
+    a.g = gy;
+    a.out = direct ? dw : ws;
+    a.split_stride = direct ? 0 : pl.pstride;
+    a.beta = direct ? beta : 0.f;
+    int rc = KATSU_E_INVALID;
+    switch (pl.variant) {
+#define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC)                                   \
+    case id: {                                                                       \
+        using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;                              \
+        auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC>;                   \
+        if ((rc = lds_optin(kern, Geo::kBytes)) != KATSU_OK) return rc;              \
+        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a);          \
+        rc = launch_status();                                                        \
+        break;                                                                       \
+    }
+        KATSU_DW_VARIANTS(KATSU_DW_CASE)
+#undef KATSU_DW_CASE
+        default: return KATSU_E_INVALID;
+    }
+    if (rc != KATSU_OK || direct) return rc;
+    constexpr int G = 8;
+    const int64_t elems = (int64_t)a.K * a.CRS;
+    const int64_t per_block = (256 / G) * 4;
+    dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, per_block)), dim3(256), 0, st>>>(
+        ws, dw, elems, pl.pstride, pl.splits, beta);
+    return launch_status();
+}
+
+// ---------------------------------------------------------------------------
 // Forward.
 
 template <class C>
@@ -291,6 +527,12 @@ int conv_fwd_dev(const float *x, const float *w, float *y, const katsu_conv_geom
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
     if (d.npix_out == 0) return KATSU_OK;
     if (!x || !w || !y) return KATSU_E_INVALID;
+    {
+        DirectFwdProblem P{x, w, y, d.N, d.C, d.H, d.W, d.K, d.R, d.S, d.st, d.pad, d.pad,
+                           d.OH, d.OW, 0.f};
+        int rc = KATSU_OK;
+        if (direct_fwd<0>(P, st, &rc)) return rc;
+    }
     if (d.K <= 16) return fwd_cfg<CfgS>(x, w, y, d, st);
     if (d.K <= 64) return fwd_cfg<CfgM>(x, w, y, d, st);
     return fwd_cfg<CfgL>(x, w, y, d, st);
@@ -375,6 +617,14 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
     if (d.npix_in == 0) return KATSU_OK;
     if (!gy || !w || !dx) return KATSU_E_INVALID;
+    // Stride 1: dX is a forward convolution of G with the transposed, flipped
+    // filter and padding R-1-pad (rows) / S-1-pad (columns).
+    if (d.st == 1 && d.pad <= d.R - 1 && d.pad <= d.S - 1) {
+        DirectFwdProblem P{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1,
+                           d.R - 1 - d.pad, d.S - 1 - d.pad, d.H, d.W, beta};
+        int rc = KATSU_OK;
+        if (direct_fwd<1>(P, st, &rc)) return rc;
+    }
     if (d.C <= 16) return dx_cfg<CfgS>(gy, w, dx, d, beta, st);
     if (d.C <= 64) return dx_cfg<CfgM>(gy, w, dx, d, beta, st);
     return dx_cfg<CfgL>(gy, w, dx, d, beta, st);
@@ -386,6 +636,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
 struct DwPlan {
     int tiles_m, tiles_n, splits, kchunk;
     size_t ws_bytes;
+    DirectDwPlan direct;  // used when direct.ok
 };
 
 template <class C>
@@ -409,7 +660,16 @@ DwPlan dw_plan(const ConvDims &d) {
     return pl;
 }
 
-DwPlan dw_plan_any(const ConvDims &d) { return dw_plan<CfgW>(d); }
+DwPlan dw_plan_any(const ConvDims &d) {
+    DirectDwPlan dp = direct_dw_plan_any(d);
+    if (dp.ok) {
+        DwPlan pl{};
+        pl.ws_bytes = dp.ws_bytes;
+        pl.direct = dp;
+        return pl;
+    }
+    return dw_plan<CfgW>(d);
+}
 
 template <class C>
 int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float beta,
@@ -480,6 +740,7 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
             return KATSU_E_INVALID;
         }
     }
+    if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 
