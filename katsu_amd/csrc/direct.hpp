@@ -260,6 +260,11 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
 // the X halo [CT][ROWS][64*CC] for each tile through a two-stage LDS
 // pipeline, and writes one partial dw[KT][CT][R][S] at the end.  Waves split
 // KT x CT into 16 x 16 slices.
+//
+// A tile is `trows` whole output rows, or one segment of `seg_w` columns of
+// a row: either way its G pixels are contiguous in memory.  A k-step takes
+// four consecutive columns of one tile row, so the step geometry is uniform
+// (scalar) and only the lane's column is per-lane.
 struct DirectDwArgs {
     const float *x;    // [N][C][H][W]
     const float *g;    // [N][K][OH][OW]
@@ -267,12 +272,15 @@ struct DirectDwArgs {
     int N, C, H, W, K, OH, OW, st, pad;
     int OHW, HW, CRS;
     int64_t x_img, g_img;
-    int tile_px, tiles_img, tiles_total, tiles_per_split;
+    int trows;           // output rows per tile (1 when tiles are row segments)
+    int seg_w;           // columns per tile (OW when tiles are whole rows)
+    int segs;            // tiles per row band: cdiv(OW, seg_w)
+    int tiles_img, tiles_total, tiles_per_split;
     int k_blocks, c_blocks;
     int ncols;
     int64_t split_stride;  // floats between partials, or 0 when writing dw directly
     float beta;            // applied only when writing dw directly
-    FastDiv fd_ow, fd_tiles_img;
+    FastDiv fd_tiles_img, fd_segs;
 };
 
 template <int KT, int CT, int ROWS, int CC, int GPC>
@@ -286,7 +294,7 @@ struct DirectDwGeo {
 };
 
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
-__global__ void __launch_bounds__(256) direct_dw_kernel(const DirectDwArgs a) {
+__global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
     using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
     constexpr int RS = R * S;
     constexpr int WK = KT / 16;         // waves along output channels
@@ -320,19 +328,23 @@ __global__ void __launch_bounds__(256) direct_dw_kernel(const DirectDwArgs a) {
     float xr[CPW][ROWS][CC];
     float gr[GRW][GPC];
 
-    struct TileGeo { int n, p0, np, oy0; };
+    struct TileGeo { int n, oy0, tr, cx0, cx1, np; };
     auto geo = [&](int tile) __attribute__((always_inline)) {
         TileGeo tg;
         tg.n = a.fd_tiles_img.div(tile);
-        tg.p0 = (tile - tg.n * a.tiles_img) * a.tile_px;
-        tg.np = min(a.tile_px, a.OHW - tg.p0);
-        tg.oy0 = a.fd_ow.div(tg.p0);
+        const int ti = tile - tg.n * a.tiles_img;
+        const int band = a.fd_segs.div(ti);
+        tg.oy0 = band * a.trows;
+        tg.tr = min(a.trows, a.OH - tg.oy0);
+        tg.cx0 = (ti - band * a.segs) * a.seg_w;
+        tg.cx1 = min(tg.cx0 + a.seg_w, a.OW);
+        tg.np = tg.tr * (tg.cx1 - tg.cx0);
         return tg;
     };
 
     auto load = [&](const TileGeo &tg) __attribute__((always_inline)) {
         const float *xb = a.x + (int64_t)tg.n * a.x_img;
-        const float *gb = a.g + (int64_t)tg.n * a.g_img + tg.p0;
+        const float *gb = a.g + (int64_t)tg.n * a.g_img + tg.oy0 * a.OW + tg.cx0;
         const int iy0 = tg.oy0 * a.st - a.pad;
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
@@ -348,7 +360,7 @@ __global__ void __launch_bounds__(256) direct_dw_kernel(const DirectDwArgs a) {
                     xr[j][r][c] = (rok && colok[c]) ? src[iy * a.W + colx[c]] : 0.f;
             }
         }
-        // G rows k0 + wave + 4i, pixels lane + 64c of the tile.
+        // G rows k0 + wave + 4i, tile pixels lane + 64c (contiguous in memory).
 #pragma unroll
         for (int i = 0; i < GRW; ++i) {
             const int k = k0 + wave + 4 * i;
@@ -382,28 +394,51 @@ __global__ void __launch_bounds__(256) direct_dw_kernel(const DirectDwArgs a) {
 #pragma unroll
     for (int i = 0; i < RS; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int arow = (wk * 16 + (lane & 15)) * Geo::GPITCH + (lane >> 4);
+    const int arow = (wk * 16 + (lane & 15)) * Geo::GPITCH;
     const int bch = Geo::GS + (wc * 16 + (lane & 15)) * Geo::CPITCH;
+    const int lq = lane >> 4;  // the lane's pixel within a k-step
 
-    // One k-step covers pixels q0..q0+3 of the tile; lanes beyond the tile
-    // contribute exact zeros (both operands zeroed).
+    // One stage: k-steps over (tile row, 4-column group), two register sets
+    // so the fragments of step s+1 are read while step s's MFMAs run.  A lane
+    // past the end of its tile row reads the row's last pixel (finite data)
+    // and its G value is zeroed at MFMA time, so it contributes nothing; the
+    // mask is applied after the next step's reads are issued, keeping the
+    // LDS latency off the MFMA path.
     auto compute = [&](const float *base, const TileGeo &tg) __attribute__((always_inline)) {
-        for (int q0 = 0; q0 < tg.np; q0 += 4) {
-            const int q = q0 + (lane >> 4);
-            const bool ok = q < tg.np;
-            const int p = tg.p0 + (ok ? q : 0);
-            const int oy = a.fd_ow.div(p);
-            const int ox = p - oy * a.OW;
-            const float *xs = base + bch + (oy - tg.oy0) * a.st * Geo::PITCH + ox * a.st;
-            const float ag = base[arow + q0];
-            const float av = ok ? ag : 0.f;
+        const int wseg = tg.cx1 - tg.cx0;
+        const int cpr = (wseg + 3) >> 2;
+        const int nsteps = tg.tr * cpr;
+        int fr = 0, fc = 0;  // (tile row, column group) of the next step to fetch
+        auto fetch = [&](float &av, float (&b)[RS], bool &ok) __attribute__((always_inline)) {
+            const int row = min(fr, tg.tr - 1);  // a fetch past the last step re-reads it
+            const int col = tg.cx0 + fc * 4 + lq;
+            ok = col < tg.cx1;
+            const int cc = min(col, tg.cx1 - 1);
+            av = base[arow + row * wseg + (cc - tg.cx0)];
+            const float *xs = base + bch + row * a.st * Geo::PITCH + cc * a.st;
 #pragma unroll
-            for (int tap = 0; tap < RS; ++tap) {
-                const int r = tap / S, s = tap % S;
-                const float bx = xs[r * Geo::PITCH + s];
-                const float bv = ok ? bx : 0.f;
-                acc[tap] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[tap], 0, 0, 0);
+            for (int tap = 0; tap < RS; ++tap) b[tap] = xs[(tap / S) * Geo::PITCH + tap % S];
+            if (++fc == cpr) {
+                fc = 0;
+                ++fr;
             }
+        };
+        auto mma = [&](const float av, const float (&b)[RS], const bool ok)
+            __attribute__((always_inline)) {
+            const float am = ok ? av : 0.f;
+#pragma unroll
+            for (int tap = 0; tap < RS; ++tap)
+                acc[tap] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, b[tap], acc[tap], 0, 0, 0);
+        };
+        float a0, a1, b0[RS], b1[RS];
+        bool k0ok, k1ok;
+        fetch(a0, b0, k0ok);
+        for (int s = 0; s < nsteps; s += 2) {
+            fetch(a1, b1, k1ok);
+            mma(a0, b0, k0ok);
+            if (s + 1 >= nsteps) break;
+            fetch(a0, b0, k0ok);
+            mma(a1, b1, k1ok);
         }
     };
 

@@ -375,28 +375,19 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
     if (d.R != R || d.S != S) return false;
-    const int64_t tmax = 64 * GPC;
-    const int64_t OHW = d.OHW;
+    const int64_t tmax = 64 * GPC;  // G tile capacity (pixels)
     const int64_t ncols = (int64_t)(d.OW - 1) * d.st + S;
-    if (ncols > 64 * CC) return false;
-    // Whole output rows per tile when they fit, else a divisor of the row.
-    int64_t tile_px = 0;
+    if (ncols > 64 * CC || R > ROWS) return false;
+    // Whole output rows per tile when a row fits, else balanced row segments.
+    int64_t trows = 1, seg_w = d.OW;
     if (d.OW <= tmax) {
-        tile_px = (int64_t)d.OW * (tmax / d.OW);
+        trows = std::min<int64_t>(tmax / d.OW, (ROWS - R) / d.st + 1);
+        trows = std::max<int64_t>(1, std::min<int64_t>(trows, d.OH));
     } else {
-        for (int64_t t = tmax; t >= 16; --t)
-            if (d.OW % t == 0) {
-                tile_px = t;
-                break;
-            }
-        if (tile_px == 0) tile_px = tmax;
+        seg_w = cdiv(d.OW, cdiv(d.OW, tmax));
     }
-    tile_px = std::min<int64_t>(tile_px, OHW);
-    // Fewer rows per tile until the halo fits ROWS.
-    while (tile_px > d.OW && (tile_row_span(tile_px, d.OW, d.OH) - 1) * d.st + R > ROWS)
-        tile_px -= d.OW;
-    if ((tile_row_span(tile_px, d.OW, d.OH) - 1) * d.st + R > ROWS) return false;
-    const int64_t tiles_img = cdiv(OHW, tile_px);
+    const int64_t segs = cdiv(d.OW, seg_w);
+    const int64_t tiles_img = cdiv(d.OH, trows) * segs;
     const int64_t tiles_total = (int64_t)d.N * tiles_img;
     const int64_t kb = cdiv(d.K, KT), cb = cdiv(d.C, CT);
     int64_t splits = std::max<int64_t>(1, cdiv(kDwTargetBlocks, kb * cb));
@@ -424,7 +415,9 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     a.CRS = d.CRS;
     a.x_img = d.CHW;
     a.g_img = d.KOHW;
-    a.tile_px = (int)tile_px;
+    a.trows = (int)trows;
+    a.seg_w = (int)seg_w;
+    a.segs = (int)segs;
     a.tiles_img = (int)tiles_img;
     a.tiles_total = (int)tiles_total;
     a.tiles_per_split = (int)tps;
@@ -433,8 +426,8 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     a.ncols = (int)ncols;
     a.split_stride = 0;
     a.beta = 0.f;
-    a.fd_ow = fdiv(d.OW);
     a.fd_tiles_img = fdiv(tiles_img);
+    a.fd_segs = fdiv(segs);
     pl->ok = true;
     pl->blocks = blocks;
     pl->splits = (int)splits;
