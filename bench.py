@@ -21,6 +21,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+CALIB_BYTES = 256 << 20  # the traffic-calibration copy (see main)
 METRIC = ("Conv2D fwd+bwd TFLOP/s and % FP32 MFMA peak (N32 C64 56x56 3x3); "
           "matmul TFLOP/s")
 
@@ -35,7 +36,7 @@ def parse():
     ap.add_argument("--matmul-steps", type=int, default=5)
     ap.add_argument("--no-matmul", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-images", type=int, default=16,
+    ap.add_argument("--cpu-images", type=int, default=32,
                     help="images of the workload timed on the CPU oracle")
     return ap.parse_args()
 
@@ -126,6 +127,13 @@ def main():
 
     for _ in range(args.warmup):
         step()
+    # Traffic calibration: one plain device copy of CALIB_BYTES, outside the
+    # timed region.  Under `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE) its
+    # counter value is the reading for a known byte count, which scales the
+    # counters of the conv kernels to bytes.
+    calib = torch.empty(CALIB_BYTES // 4, device=dev, dtype=torch.float32)
+    calib.copy_(torch.empty_like(calib).fill_(1.0))
+    del calib
     torch.cuda.synchronize()
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]

@@ -10,6 +10,13 @@
 // parameter, so every tap, channel and pipeline-stage offset is an LDS
 // instruction immediate: the MFMA loop is LDS reads and MFMAs only.
 //
+// Global loads go through buffer resources: a lane whose element lies in the
+// padding or past a tensor edge gets an out-of-range offset and reads zero,
+// so staging has no branches.  Weight rows (and G rows in dW) are fetched
+// as 16-byte loads when the host has checked their alignment (WVEC, g_vec).
+// Block outputs are transposed through LDS and written as contiguous
+// 16-byte runs.
+//
 //   direct_fwd_kernel   out[n][co][p] = sum_{ci,r,s} in[n][ci][tap(p,r,s)] * w'(co,ci,r,s)
 //                       forward (WMODE 0: w' = w) and, for stride 1, the
 //                       data gradient (WMODE 1: in = G, w' = w transposed
@@ -25,6 +32,40 @@
 #include "igemm.hpp"
 
 namespace katsu {
+
+// Scheduling fence for a software-pipelined k-step: the LDS reads of the
+// next step (NREAD of them) are issued before the MFMAs of the current step
+// (NMFMA), so the reads' latency overlaps the MFMAs.  Without it the
+// scheduler tends to issue the reads after the MFMAs, and the next step then
+// stalls on them.  The empty asm with a memory clobber keeps the load/store
+// optimizer from fusing reads of different steps into one ds_read2, which
+// would pull a read into the step that consumes it.
+template <int NREAD, int NMFMA>
+__device__ __forceinline__ void order_reads_then_mfma() {
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);  // MFMA
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Buffer-resource loads.  Range checking of a raw buffer (stride 0) returns
+// zero for any byte offset >= the resource size, so `kOOB` (with resources
+// kept below 1 GiB by the host) turns a load into a zero without a branch.
+constexpr int kOOB = 0x40000000;
+constexpr uint32_t kMaxBufBytes = 0x40000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float *p, uint32_t bytes) {
+    // 0x00020000: the gfx9 data-format word of an untyped 32-bit buffer.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 // ---------------------------------------------------------------------------
 // Forward / data-gradient kernel.
@@ -45,12 +86,14 @@ struct DirectArgs {
     int tiles_img;     // tiles per image
     int co_blocks;     // ceil(CO / KT)
     int ncols;         // halo columns: (OW-1)*st + S  (<= 64*CC)
+    uint32_t w_bytes;  // size of w
+    int out_vec;       // 1: tile_px and OHW are multiples of 4 (16-byte output runs)
     float beta;        // out = beta*out + result (beta in {0, 1})
     FastDiv fd_ow;     // division by OW
 };
 
 // LDS layout (floats) of the forward kernel.
-template <int KT, int CB, int R, int S, int ROWS, int CC, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
 struct DirectFwdGeo {
     static constexpr int RS = R * S;
     static constexpr int PITCH = 64 * CC;               // halo row pitch
@@ -64,19 +107,27 @@ struct DirectFwdGeo {
     static constexpr int WPITCH = WMODE == 0 ? WLEN + 1 : WLEN + ((16 - WLEN % 32) + 32) % 32;
     static constexpr int WS = WROWS * WPITCH;
     static constexpr int STAGE = XS + WS;
+    // Output transpose buffer (reuses the stages after the last chunk).
+    static constexpr int TPMAX = (4 / (KT / 16)) * F * 16;  // pixels per tile, at most
+    static constexpr int YPITCH = TPMAX + 4;
+    static_assert(KT * YPITCH <= 2 * STAGE, "output tile must fit the LDS stages");
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
 };
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE, bool WVEC>
 __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
-    using Geo = DirectFwdGeo<KT, CB, R, S, ROWS, CC, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
     constexpr int RS = R * S;
     constexpr int WOC = KT / 16;            // waves along output channels
-    constexpr int TPR = 256 / Geo::WROWS;   // threads per weight row
-    constexpr int WPT = (Geo::WLEN + TPR - 1) / TPR;  // weight floats per thread
     constexpr int CPW = CB / 4;             // input channels staged per wave
+    // Weight staging: scalar (TPR threads per row) or 16-byte (float4 per lane).
+    constexpr int TPR = 256 / Geo::WROWS;
+    constexpr int WPT = (Geo::WLEN + TPR - 1) / TPR;
+    constexpr int W4ROW = Geo::WLEN / 4;                       // float4 per row
+    constexpr int WQ4 = (Geo::WROWS * W4ROW + 255) / 256;      // float4 per thread
     static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
     static_assert(CB % 4 == 0 && 256 % Geo::WROWS == 0, "CB must be a multiple of 4");
+    static_assert(!WVEC || Geo::WLEN % 4 == 0, "16-byte weight rows");
 
     extern __shared__ float smem[];
 
@@ -110,55 +161,75 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
 
     // ---- staging: input halo rows ------------------------------------------
     // Wave w stages channels w + 4j (j < CPW), every row, 64 columns per chunk.
-    const float *inb = a.in + (int64_t)n * a.in_img;
-    bool colok[CC];
-    int colx[CC];
+    const __amdgpu_buffer_rsrc_t rin =
+        buf_rsrc(a.in + (int64_t)n * a.in_img, (uint32_t)(a.in_img * 4));
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, a.w_bytes);
+    int colb[CC];  // byte offset of the lane's column within a row, or kOOB
 #pragma unroll
     for (int c = 0; c < CC; ++c) {
         const int col = c * 64 + lane;
-        colx[c] = col - a.padx;
-        colok[c] = col < a.ncols && (unsigned)colx[c] < (unsigned)a.W;
+        const int ix = col - a.padx;
+        colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
     float xr[CPW][ROWS][CC];
 
     // ---- staging: weights ----------------------------------------------------
     const int wrow = tid / TPR, wcol = tid % TPR;
-    float wr[WPT];
+    float wr[WVEC ? 1 : WPT];
+    floatx4 wr4[WVEC ? WQ4 : 1];
 
     auto load = [&](int ci0) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
             const int ci = ci0 + wave + 4 * j;
-            const bool cok = ci < a.CI;
-            const float *src = inb + (int64_t)ci * a.HW;
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const int iy = iy0 + r;
-                const bool rok = cok && (unsigned)iy < (unsigned)a.H;
+                const bool rok = ci < a.CI && (unsigned)iy < (unsigned)a.H;
+                const int rowb = (ci * a.H + iy) * a.W * 4;
 #pragma unroll
                 for (int c = 0; c < CC; ++c)
-                    xr[j][r][c] = (rok && colok[c]) ? src[iy * a.W + colx[c]] : 0.f;
+                    xr[j][r][c] = buf_load(rin, rok ? rowb + colb[c] : kOOB);
             }
         }
-        if (WMODE == 0) {
-            // row co = co0 + wrow: CB*RS contiguous floats from w[co][ci0][0][0].
-            const int co = co0 + wrow;
-            const int lim = co < a.CO ? min(CB, a.CI - ci0) * RS : 0;
-            const float *src = a.w + ((int64_t)co * a.CI + ci0) * RS;
+        if (WVEC) {
+            // Flat float4 index over WROWS rows of WLEN floats; lim = valid
+            // floats of a row (partial last chunk, channels past the count).
 #pragma unroll
-            for (int q = 0; q < WPT; ++q) {
-                const int e = wcol + TPR * q;
-                wr[q] = (e < lim && e < Geo::WLEN) ? src[e] : 0.f;
+            for (int q = 0; q < WQ4; ++q) {
+                const int e4 = q * 256 + tid;
+                const int row = e4 / W4ROW, c4 = e4 - (e4 / W4ROW) * W4ROW;
+                int off = kOOB;
+                if (WMODE == 0) {
+                    const int co = co0 + row;
+                    const int lim = min(CB, a.CI - ci0) * RS;
+                    if (row < KT && co < a.CO && c4 * 4 < lim)
+                        off = (((co * a.CI + ci0) * RS) + c4 * 4) * 4;
+                } else {
+                    const int ci = ci0 + row;
+                    const int lim = min(KT, a.CO - co0) * RS;
+                    if (row < CB && ci < a.CI && c4 * 4 < lim)
+                        off = (((ci * a.CO + co0) * RS) + c4 * 4) * 4;
+                }
+                wr4[q] = buf_load4(rw, off);
             }
         } else {
-            // row ci = ci0 + wrow: KT*RS contiguous floats from w[ci][co0][0][0].
-            const int ci = ci0 + wrow;
-            const int lim = ci < a.CI ? min(KT, a.CO - co0) * RS : 0;
-            const float *src = a.w + ((int64_t)ci * a.CO + co0) * RS;
+            int rowb, lim;
+            if (WMODE == 0) {
+                // row co = co0 + wrow: CB*RS contiguous floats from w[co][ci0][0][0].
+                const int co = co0 + wrow;
+                lim = co < a.CO ? min(CB, a.CI - ci0) * RS : 0;
+                rowb = (co * a.CI + ci0) * RS * 4;
+            } else {
+                // row ci = ci0 + wrow: KT*RS contiguous floats from w[ci][co0][0][0].
+                const int ci = ci0 + wrow;
+                lim = ci < a.CI ? min(KT, a.CO - co0) * RS : 0;
+                rowb = (ci * a.CO + co0) * RS * 4;
+            }
 #pragma unroll
             for (int q = 0; q < WPT; ++q) {
                 const int e = wcol + TPR * q;
-                wr[q] = (e < lim && e < Geo::WLEN) ? src[e] : 0.f;
+                wr[q] = buf_load(rw, (e < lim && e < Geo::WLEN) ? rowb + e * 4 : kOOB);
             }
         }
     };
@@ -172,10 +243,25 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
 #pragma unroll
                 for (int c = 0; c < CC; ++c)
                     xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
-        float *ws = base + Geo::XS + wrow * Geo::WPITCH + wcol;
+        if (WVEC) {
 #pragma unroll
-        for (int q = 0; q < WPT; ++q)
-            if (wcol + TPR * q < Geo::WLEN) ws[TPR * q] = wr[q];
+            for (int q = 0; q < WQ4; ++q) {
+                const int e4 = q * 256 + tid;
+                const int row = e4 / W4ROW, c4 = e4 - (e4 / W4ROW) * W4ROW;
+                if (row < Geo::WROWS) {
+                    float *d = base + Geo::XS + row * Geo::WPITCH + c4 * 4;
+                    d[0] = wr4[q][0];
+                    d[1] = wr4[q][1];
+                    d[2] = wr4[q][2];
+                    d[3] = wr4[q][3];
+                }
+            }
+        } else {
+            float *ws = base + Geo::XS + wrow * Geo::WPITCH + wcol;
+#pragma unroll
+            for (int q = 0; q < WPT; ++q)
+                if (wcol + TPR * q < Geo::WLEN) ws[TPR * q] = wr[q];
+        }
     };
 
     floatx4 acc[F];
@@ -184,7 +270,8 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
 
     // One k-step kk = (channel quad cs, tap): the A fragment and the F B
     // fragments it multiplies.  All offsets are compile-time after unrolling.
-    auto fetch = [&](const float *base, const int kk, float (&b)[F], float &av) {
+    auto fetch = [&](const float *base, const int kk, float (&b)[F], float &av)
+        __attribute__((always_inline)) {
         const int cs = kk / RS, tap = kk % RS;
         const int r = tap / S, s = tap % S;
         const float *ws = base + Geo::XS + abase;
@@ -193,27 +280,27 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
 #pragma unroll
         for (int f = 0; f < F; ++f) b[f] = base[pix[f] + toff];
     };
-    auto mma = [&](const float (&b)[F], const float av) {
+    auto mma = [&](const float (&b)[F], const float av) __attribute__((always_inline)) {
 #pragma unroll
         for (int f = 0; f < F; ++f)
             acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[f], acc[f], 0, 0, 0);
     };
     // Software pipeline over the k-steps of one stage: the fragments of step
-    // kk+1 are read while step kk's MFMAs run.  The scheduling barriers keep
-    // the compiler from hoisting every read of the stage (register blow-up).
+    // kk+1 are read while step kk's MFMAs run.
     auto compute = [&](const float *base) __attribute__((always_inline)) {
         constexpr int NK = (CB / 4) * RS;
         float b0[F], b1[F];
         float a0, a1;
         fetch(base, 0, b0, a0);
+        asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
 #pragma unroll
         for (int kk = 0; kk < NK; kk += 2) {
             if (kk + 1 < NK) fetch(base, kk + 1, b1, a1);
             mma(b0, a0);
-            __builtin_amdgcn_sched_barrier(0);
+            order_reads_then_mfma<F + 1, F>();
             if (kk + 2 < NK) fetch(base, kk + 2, b0, a0);
             if (kk + 1 < NK) mma(b1, a1);
-            __builtin_amdgcn_sched_barrier(0);
+            order_reads_then_mfma<F + 1, F>();
         }
     };
 
@@ -238,15 +325,39 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
         __syncthreads();
     }
 
+    // Epilogue: transpose the KT x tile block through LDS (the stages are
+    // free after the last barrier), then write each output channel's pixel
+    // run -- contiguous in NCHW -- as 16-byte stores.
+    float *ys = smem;
+#pragma unroll
+    for (int f = 0; f < F; ++f)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            ys[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * 16 + (lane & 15)] =
+                acc[f][v];
+    __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
-#pragma unroll
-    for (int f = 0; f < F; ++f) {
-        const int p = p0 + (wpx * F + f) * 16 + (lane & 15);
-        if (p >= p1) continue;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int co = co0 + woc * 16 + 4 * (lane >> 4) + v;
-            if (co < a.CO) store_beta(outb + (int64_t)co * a.OHW + p, acc[f][v], a.beta);
+    const int np = p1 - p0;
+    if (a.out_vec) {
+        const int n4 = np >> 2;
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            float *dst = outb + (int64_t)co * a.OHW + p0;
+            for (int c4 = lane; c4 < n4; c4 += 64) {
+                floatx4 v = *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
+                floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
+                if (a.beta != 0.f) v += *d;
+                *d = v;
+            }
+        }
+    } else {
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            float *dst = outb + (int64_t)co * a.OHW + p0;
+            for (int p = lane; p < np; p += 64)
+                store_beta(dst + p, ys[row * Geo::YPITCH + p], a.beta);
         }
     }
 }
@@ -278,30 +389,37 @@ struct DirectDwArgs {
     int tiles_img, tiles_total, tiles_per_split;
     int k_blocks, c_blocks;
     int ncols;
+    int g_vec;           // 1: tile starts and OHW are multiples of 4 (16-byte G rows)
+    int out_vec;         // 1: partial rows are 16-byte aligned runs
     int64_t split_stride;  // floats between partials, or 0 when writing dw directly
     float beta;            // applied only when writing dw directly
     FastDiv fd_tiles_img, fd_segs;
 };
 
-template <int KT, int CT, int ROWS, int CC, int GPC>
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
 struct DirectDwGeo {
     static constexpr int PITCH = 64 * CC;
     static constexpr int CPITCH = ROWS * PITCH + 2;   // == 2 (mod 32)
     static constexpr int GPITCH = 64 * GPC + 2;       // == 2 (mod 32)
     static constexpr int GS = KT * GPITCH;
     static constexpr int STAGE = GS + CT * CPITCH;
+    static constexpr int PPITCH = CT * R * S + 4;     // partial transpose buffer
+    static_assert(KT * PPITCH <= 2 * STAGE, "partial tile must fit the LDS stages");
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
 };
 
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
 __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
-    using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
+    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
     constexpr int RS = R * S;
     constexpr int WK = KT / 16;         // waves along output channels
     constexpr int CPW = CT / 4;         // input channels staged per wave
-    constexpr int GRW = KT / 4;         // G rows staged per wave
+    constexpr int GRW = KT / 4;         // G rows staged per wave (scalar path)
+    constexpr int G4 = 16 * GPC;        // float4 per G tile row, at most
+    constexpr int GQ4 = KT * G4 / 256;  // float4 G loads per thread
     static_assert(KT % 16 == 0 && CT % 16 == 0 && (KT / 16) * (CT / 16) == 4,
                   "4 waves of 16x16 slices");
+    static_assert((KT * G4) % 256 == 0, "G tile must split evenly over the block");
 
     extern __shared__ float smem[];
 
@@ -317,16 +435,16 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     const int tb = split * a.tiles_per_split;
     const int te = min(tb + a.tiles_per_split, a.tiles_total);
 
-    bool colok[CC];
-    int colx[CC];
+    int colb[CC];
 #pragma unroll
     for (int c = 0; c < CC; ++c) {
         const int col = c * 64 + lane;
-        colx[c] = col - a.pad;
-        colok[c] = col < a.ncols && (unsigned)colx[c] < (unsigned)a.W;
+        const int ix = col - a.pad;
+        colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
     float xr[CPW][ROWS][CC];
-    float gr[GRW][GPC];
+    float gr[GRW * GPC];  // scalar G path
+    floatx4 gr4[GQ4];     // 16-byte G path
 
     struct TileGeo { int n, oy0, tr, cx0, cx1, np; };
     auto geo = [&](int tile) __attribute__((always_inline)) {
@@ -343,43 +461,66 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     };
 
     auto load = [&](const TileGeo &tg) __attribute__((always_inline)) {
-        const float *xb = a.x + (int64_t)tg.n * a.x_img;
-        const float *gb = a.g + (int64_t)tg.n * a.g_img + tg.oy0 * a.OW + tg.cx0;
+        const __amdgpu_buffer_rsrc_t rx =
+            buf_rsrc(a.x + (int64_t)tg.n * a.x_img, (uint32_t)(a.x_img * 4));
+        const __amdgpu_buffer_rsrc_t rg =
+            buf_rsrc(a.g + (int64_t)tg.n * a.g_img, (uint32_t)(a.g_img * 4));
         const int iy0 = tg.oy0 * a.st - a.pad;
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
             const int ci = c0 + wave + 4 * j;
-            const bool cok = ci < a.C;
-            const float *src = xb + (int64_t)ci * a.HW;
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const int iy = iy0 + r;
-                const bool rok = cok && (unsigned)iy < (unsigned)a.H;
+                const bool rok = ci < a.C && (unsigned)iy < (unsigned)a.H;
+                const int rowb = (ci * a.H + iy) * a.W * 4;
 #pragma unroll
                 for (int c = 0; c < CC; ++c)
-                    xr[j][r][c] = (rok && colok[c]) ? src[iy * a.W + colx[c]] : 0.f;
+                    xr[j][r][c] = buf_load(rx, rok ? rowb + colb[c] : kOOB);
             }
         }
-        // G rows k0 + wave + 4i, tile pixels lane + 64c (contiguous in memory).
+        // G rows k0..k0+KT of the tile (contiguous pixels from p0).
+        const int p0 = tg.oy0 * a.OW + tg.cx0;
+        if (a.g_vec) {
 #pragma unroll
-        for (int i = 0; i < GRW; ++i) {
-            const int k = k0 + wave + 4 * i;
-            const bool kok = k < a.K;
-            const float *src = gb + (int64_t)k * a.OHW;
+            for (int q = 0; q < GQ4; ++q) {
+                const int e4 = q * 256 + tid;
+                const int row = e4 / G4, c4 = e4 % G4;
+                const int k = k0 + row;
+                const bool ok = k < a.K && c4 * 4 < tg.np;
+                gr4[q] = buf_load4(rg, ok ? (k * a.OHW + p0 + c4 * 4) * 4 : kOOB);
+            }
+        } else {
 #pragma unroll
-            for (int c = 0; c < GPC; ++c) {
-                const int px = c * 64 + lane;
-                gr[i][c] = (kok && px < tg.np) ? src[px] : 0.f;
+            for (int i = 0; i < GRW; ++i) {
+                const int k = k0 + wave + 4 * i;
+#pragma unroll
+                for (int c = 0; c < GPC; ++c) {
+                    const int px = c * 64 + lane;
+                    const bool ok = k < a.K && px < tg.np;
+                    gr[i * GPC + c] = buf_load(rg, ok ? (k * a.OHW + p0 + px) * 4 : kOOB);
+                }
             }
         }
     };
 
     auto store = [&](float *base) __attribute__((always_inline)) {
-        float *gs = base + wave * Geo::GPITCH + lane;
+        if (a.g_vec) {
 #pragma unroll
-        for (int i = 0; i < GRW; ++i)
+            for (int q = 0; q < GQ4; ++q) {
+                const int e4 = q * 256 + tid;
+                const int row = e4 / G4, c4 = e4 % G4;
+                float *d = base + row * Geo::GPITCH + c4 * 4;  // 8-byte aligned
+                *reinterpret_cast<float2 *>(d) = make_float2(gr4[q][0], gr4[q][1]);
+                *reinterpret_cast<float2 *>(d + 2) = make_float2(gr4[q][2], gr4[q][3]);
+            }
+        } else {
+            float *gs = base + wave * Geo::GPITCH + lane;
 #pragma unroll
-            for (int c = 0; c < GPC; ++c) gs[4 * i * Geo::GPITCH + c * 64] = gr[i][c];
+            for (int i = 0; i < GRW; ++i)
+#pragma unroll
+                for (int c = 0; c < GPC; ++c) gs[4 * i * Geo::GPITCH + c * 64] = gr[i * GPC + c];
+        }
         float *xs = base + Geo::GS + wave * Geo::CPITCH + lane;
 #pragma unroll
         for (int j = 0; j < CPW; ++j)
@@ -433,12 +574,15 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
         float a0, a1, b0[RS], b1[RS];
         bool k0ok, k1ok;
         fetch(a0, b0, k0ok);
+        asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
         for (int s = 0; s < nsteps; s += 2) {
             fetch(a1, b1, k1ok);
             mma(a0, b0, k0ok);
+            order_reads_then_mfma<RS + 1, RS>();
             if (s + 1 >= nsteps) break;
             fetch(a0, b0, k0ok);
             mma(a1, b1, k1ok);
+            order_reads_then_mfma<RS + 1, RS>();
         }
     };
 
@@ -471,21 +615,37 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
         }
     }
 
-    // D[i = oc][j = c] per tap -> out[split][oc][c][tap].
+    // Epilogue: D[i = oc][j = c] per tap, transposed through LDS into the
+    // partial's row order [oc][c][tap], then written as contiguous runs of
+    // CT*RS floats per output channel.
+    float *ps = smem;
+#pragma unroll
+    for (int tap = 0; tap < RS; ++tap)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            ps[(wk * 16 + 4 * (lane >> 4) + v) * Geo::PPITCH + (wc * 16 + (lane & 15)) * RS + tap] =
+                acc[tap][v];
+    __syncthreads();
     float *ob = a.out + (int64_t)split * a.split_stride;
-    const int c = c0 + wc * 16 + (lane & 15);
-    if (c < a.C) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int k = k0 + wk * 16 + 4 * (lane >> 4) + v;
-            if (k >= a.K) continue;
-            float *dst = ob + (int64_t)k * a.CRS + c * RS;
-#pragma unroll
-            for (int tap = 0; tap < RS; ++tap) {
+    const int len = min(CT, a.C - c0) * RS;  // valid floats of a row
+    for (int row = wave; row < KT; row += 4) {
+        const int k = k0 + row;
+        if (k >= a.K) break;
+        float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
+        const float *src = ps + row * Geo::PPITCH;
+        if (a.out_vec && len == CT * RS) {
+            for (int c4 = lane; c4 < CT * RS / 4; c4 += 64) {
+                floatx4 v = *reinterpret_cast<const floatx4 *>(src + c4 * 4);
+                floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
+                if (a.split_stride == 0 && a.beta != 0.f) v += *d;
+                *d = v;
+            }
+        } else {
+            for (int e = lane; e < len; e += 64) {
                 if (a.split_stride == 0)
-                    store_beta(dst + tap, acc[tap][v], a.beta);
+                    store_beta(dst + e, src[e], a.beta);
                 else
-                    dst[tap] = acc[tap][v];
+                    dst[e] = src[e];
             }
         }
     }

@@ -274,18 +274,14 @@ int64_t tile_row_span(int64_t tile_px, int64_t OW, int64_t OH) {
     return std::min(span, OH);
 }
 
-// Dynamic LDS above 64 KiB must be opted into once per kernel.
-template <class K>
-int lds_optin(K kernel, size_t bytes) {
+// Dynamic LDS above 64 KiB must be opted into, once per kernel function
+// (a function-local static: thread-safe one-time initialisation).
+template <auto Kernel>
+int lds_optin(size_t bytes) {
     if (bytes <= 65536) return KATSU_OK;
-    static bool done = false;  // one flag per kernel instantiation
-    if (!done) {
-        if (hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)bytes) != hipSuccess)
-            return KATSU_E_LAUNCH;
-        done = true;
-    }
-    return KATSU_OK;
+    static const hipError_t e = hipFuncSetAttribute(
+        (const void *)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    return e == hipSuccess ? KATSU_OK : KATSU_E_LAUNCH;
 }
 
 // A "forward-shaped" problem: out[n][co] = sum_ci,taps in[n][ci] * w'.
@@ -296,21 +292,30 @@ struct DirectFwdProblem {
     float beta;
 };
 
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
 bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
-    using Geo = DirectFwdGeo<KT, CB, R, S, ROWS, CC, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
     if (P.R != R || P.S != S) return false;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
     constexpr int WPX = 4 / (KT / 16);
     const int64_t OHW = P.OH * P.OW;
     const int64_t ncols = (P.OW - 1) * P.st + S;
     if (ncols > 64 * CC) return false;
+    // Buffer resources address one image of `in` and all of `w` in bytes.
+    const int64_t in_img = P.CI * P.H * P.W;
+    const int64_t w_elems = P.CO * P.CI * R * S;
+    if (in_img * 4 >= (int64_t)kMaxBufBytes || w_elems * 4 >= (int64_t)kMaxBufBytes) return false;
     const int64_t co_blocks = cdiv(P.CO, KT);
     const int64_t tpmax = (int64_t)WPX * F * 16;
-    // The fewest tiles that fit, but enough blocks to fill the chip.
+    // The fewest tiles that fit, but enough blocks to fill the chip; tile
+    // lengths rounded to whole 16-byte output runs when that still fits.
     int64_t tiles_img = std::max(cdiv(OHW, tpmax), cdiv(kMinDirectBlocks, co_blocks * P.N));
     for (int attempt = 0; attempt < 64; ++attempt, ++tiles_img) {
-        const int64_t tile_px = cdiv(OHW, tiles_img);
+        int64_t tile_px = cdiv(OHW, tiles_img);
+        if (tile_px % 4 != 0 && (tile_px + 3) / 4 * 4 <= tpmax) tile_px = (tile_px + 3) / 4 * 4;
+        if (tile_px > tpmax) continue;
         if (2 * tile_px < tpmax) return false;  // fragments would be under half full
         const int64_t ntiles = cdiv(OHW, tile_px);
         const int64_t rows_max = (tile_row_span(tile_px, P.OW, P.OH) - 1) * P.st + R;
@@ -333,17 +338,28 @@ bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
         a.padx = (int)P.padx;
         a.OHW = (int)OHW;
         a.HW = (int)(P.H * P.W);
-        a.in_img = P.CI * P.H * P.W;
+        a.in_img = in_img;
         a.out_img = P.CO * OHW;
         a.tile_px = (int)tile_px;
         a.tiles_img = (int)ntiles;
         a.co_blocks = (int)co_blocks;
         a.ncols = (int)ncols;
+        a.w_bytes = (uint32_t)(w_elems * 4);
+        a.out_vec = (tile_px % 4 == 0 && OHW % 4 == 0 && aligned16(P.out)) ? 1 : 0;
         a.beta = P.beta;
         a.fd_ow = fdiv(P.OW);
-        auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE>;
-        if ((*rc = lds_optin(kern, Geo::kBytes)) != KATSU_OK) return true;
-        kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
+        // 16-byte weight rows: every row start must be 16-byte aligned.
+        const bool wvec = (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w) &&
+                          (CB * R * S) % 4 == 0 && (KT * R * S) % 4 == 0;
+        if (wvec) {
+            constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, true>;
+            if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
+            kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
+        } else {
+            constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, false>;
+            if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
+            kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
+        }
         *rc = launch_status();
         return true;
     }
@@ -372,12 +388,15 @@ constexpr int64_t kDwTargetBlocks = 512;
 
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
 bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
-    using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;
+    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
     if (d.R != R || d.S != S) return false;
     const int64_t tmax = 64 * GPC;  // G tile capacity (pixels)
     const int64_t ncols = (int64_t)(d.OW - 1) * d.st + S;
     if (ncols > 64 * CC || R > ROWS) return false;
+    // Buffer resources address one image of x and of G in bytes.
+    if ((int64_t)d.CHW * 4 >= (int64_t)kMaxBufBytes || (int64_t)d.KOHW * 4 >= (int64_t)kMaxBufBytes)
+        return false;
     // Whole output rows per tile when a row fits, else balanced row segments.
     int64_t trows = 1, seg_w = d.OW;
     if (d.OW <= tmax) {
@@ -424,6 +443,11 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     a.k_blocks = (int)kb;
     a.c_blocks = (int)cb;
     a.ncols = (int)ncols;
+    // 16-byte G rows need every tile start (a multiple of trows*OW, or of
+    // seg_w within a row) and OHW to be multiples of 4; pointer alignment is
+    // checked at launch.
+    a.g_vec = (d.OHW % 4 == 0 && (trows * d.OW) % 4 == 0 && (segs == 1 || seg_w % 4 == 0)) ? 1 : 0;
+    a.out_vec = d.CRS % 4 == 0 ? 1 : 0;
     a.split_stride = 0;
     a.beta = 0.f;
     a.fd_tiles_img = fdiv(tiles_img);
@@ -459,13 +483,15 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
     a.out = direct ? dw : ws;
     a.split_stride = direct ? 0 : pl.pstride;
     a.beta = direct ? beta : 0.f;
+    if (!aligned16(gy)) a.g_vec = 0;
+    if (!aligned16(a.out)) a.out_vec = 0;
     int rc = KATSU_E_INVALID;
     switch (pl.variant) {
 #define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC)                                   \
     case id: {                                                                       \
-        using Geo = DirectDwGeo<KT, CT, ROWS, CC, GPC>;                              \
-        auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC>;                   \
-        if ((rc = lds_optin(kern, Geo::kBytes)) != KATSU_OK) return rc;              \
+        using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;                        \
+        constexpr auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC>;         \
+        if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;              \
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a);          \
         rc = launch_status();                                                        \
         break;                                                                       \
