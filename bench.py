@@ -223,6 +223,22 @@ def main():
                          "pct_fp32_mfma_peak": round(100 * mflops / (mms * 1e-3) / 1e12
                                                      / PEAK_FP32_MFMA_TFLOPS, 2)}
 
+    # The drop-in host-buffer entry points (katsu_amd.host): each pass copies
+    # its operands in and its result out over PCIe.  Reported beside `value`,
+    # never as it.
+    from katsu_amd import host
+    gh = np.ones(yshape, np.float32)
+    host.conv2d_forward(x, w, st, pad)  # warm the staging pool
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        host.conv2d_forward(x, w, st, pad)
+        host.conv2d_backward(x, w, gh, st, pad)
+    host_ms = (time.perf_counter() - t0) / reps * 1e3
+    out["host_buffer_path"] = {"ms_per_step": round(host_ms, 3),
+                               "tflops": round(step_flops / (host_ms * 1e-3) / 1e12, 3),
+                               "note": "host-pointer ABI, PCIe copies included"}
+
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
                                            step_flops / cfg["x"][0])
