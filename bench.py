@@ -4,10 +4,14 @@ Headline workload: Conv2D forward + dX + dW on
 x [32,64,56,56] U[-1,1), w [64,64,3,3] He-normal, stride 1, padding 1,
 upstream gradient all-ones.  One step = one forward, one backward-data and one
 backward-filter pass (the latter includes its split-K reduce), inputs already
-resident in HBM.  Also reported: matmul 4096 forward + dA + dB (config 2).
+resident in HBM.  Also reported: matmul forward + dA + dB at 512, 1024 and
+4096 (config 2).
 
-Prints ONE JSON line.  Timing uses HIP events recorded on the stream the
-kernels are launched on (torch's current stream, passed to the C ABI).
+Prints ONE JSON line.  The step, each pass and each matmul step are captured
+as HIP graphs on torch's capture stream (the C ABI launches on the stream it
+is given) and replayed between HIP events, so the timings are GPU time, not
+Python launch overhead; the step's replays are checked against the eager
+result.
 """
 import argparse
 import json
@@ -22,6 +26,7 @@ sys.path.insert(0, ROOT)
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 CALIB_BYTES = 256 << 20  # the traffic-calibration copy (see main)
+PASS_REPS = 10           # launches per per-pass timing graph
 METRIC = ("Conv2D fwd+bwd TFLOP/s and % FP32 MFMA peak (N32 C64 56x56 3x3); "
           "matmul TFLOP/s")
 
@@ -32,13 +37,22 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3_resnet")
-    ap.add_argument("--matmul-n", type=int, default=4096)
+    ap.add_argument("--matmul-n", type=int, nargs="+", default=[512, 1024, 4096])
     ap.add_argument("--matmul-steps", type=int, default=5)
     ap.add_argument("--no-matmul", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-images", type=int, default=32,
                     help="images of the workload timed on the CPU oracle")
     return ap.parse_args()
+
+
+def capture(fn):
+    """A HIP graph of the launches fn makes on torch's current stream."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
 
 
 def cpu_model():
@@ -112,21 +126,24 @@ def main():
     pass_flops = synth.conv_flops(cfg)
     step_flops = 3 * pass_flops
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record()
+    def fwd():
         ops.conv2d_forward(xd, wd, st, pad, out=yd)
-        if ev is not None:
-            ev[1].record()
+
+    def bwd_data():
         ops.conv2d_backward_data(gd, wd, x.shape, st, pad, out=dxd)
-        if ev is not None:
-            ev[2].record()
+
+    def bwd_filter():
         ops.conv2d_backward_filter(xd, gd, w.shape, st, pad, out=dwd, workspace=ws)
-        if ev is not None:
-            ev[3].record()
+
+    def step():
+        fwd()
+        bwd_data()
+        bwd_filter()
 
     for _ in range(args.warmup):
         step()
+    torch.cuda.synchronize()
+    eager = (yd.clone(), dxd.clone(), dwd.clone())
     # Traffic calibration: one plain device copy of CALIB_BYTES, outside the
     # timed region.  Under `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE) its
     # counter value is the reading for a known byte count, which scales the
@@ -136,28 +153,43 @@ def main():
     del calib
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
-              for _ in range(args.steps)]
+    # The step and each pass are captured as HIP graphs (the library launches
+    # on torch's current stream, which is the capture stream), so the timed
+    # region measures the GPU, not Python's launch overhead.
+    g_step = capture(step)
+    # Per-pass graphs hold PASS_REPS back-to-back launches of the pass, so the
+    # graph-launch overhead is spread over them.
+    g_pass = {name: capture(lambda fn=fn: [fn() for _ in range(PASS_REPS)])
+              for name, fn in (("fwd", fwd), ("bwd_data", bwd_data), ("bwd_filter", bwd_filter))}
+
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
-    for i in range(args.steps):
-        step(events[i])
+    for _ in range(args.steps):
+        g_step.replay()
     end.record()
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms_per_step = total_ms / args.steps
-    per = {"fwd": [], "bwd_data": [], "bwd_filter": []}
-    for ev in events:
-        per["fwd"].append(ev[0].elapsed_time(ev[1]))
-        per["bwd_data"].append(ev[1].elapsed_time(ev[2]))
-        per["bwd_filter"].append(ev[2].elapsed_time(ev[3]))
+    ms_per_step = start.elapsed_time(end) / args.steps
+    # Every replay must reproduce the eager step bit for bit (the kernels are
+    # deterministic and the step overwrites its outputs).
+    for got, ref, name in zip((yd, dxd, dwd), eager, ("y", "dx", "dw")):
+        if not torch.equal(got, ref):
+            raise SystemExit(f"bench.py: graph replay of the step changed {name}")
+
     kernels = {}
-    for name, ts in per.items():
-        avg = float(np.mean(ts))
+    for name, g in g_pass.items():
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        avg = e0.elapsed_time(e1) / (args.steps * PASS_REPS)
         kernels[name] = {"avg_us": round(avg * 1e3, 2),
-                         "median_us": round(float(np.median(ts)) * 1e3, 2),
                          "tflops": round(pass_flops / (avg * 1e-3) / 1e12, 2)}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"])
     dom_avg_s = kernels[dominant]["avg_us"] * 1e-6
@@ -195,33 +227,40 @@ def main():
     }
 
     if not args.no_matmul:
-        n = args.matmul_n
-        a = torch.from_numpy(synth.uniform(synth.SEED_X, (n, n))).to(dev)
-        b = torch.from_numpy(synth.uniform(synth.SEED_W, (n, n))).to(dev)
-        g = torch.ones((n, n), device=dev)
-        c = torch.empty((n, n), device=dev)
-        da = torch.zeros_like(a)
-        db = torch.zeros_like(b)
+        # Config 2: C = A.B then dA += G.B^T, dB += A^T.G (loss = sum(C), so
+        # G = 1), for each size; graph replays as for the convolution step.
+        out["matmul"] = {}
+        for n in args.matmul_n:
+            a = torch.from_numpy(synth.uniform(synth.SEED_X, (n, n))).to(dev)
+            b = torch.from_numpy(synth.uniform(synth.SEED_W, (n, n))).to(dev)
+            g = torch.ones((n, n), device=dev)
+            c = torch.empty((n, n), device=dev)
+            da = torch.zeros_like(a)
+            db = torch.zeros_like(b)
 
-        def mstep():
-            ops.gemm(a, b, n, n, n, out=c)
-            ops.matmul_vjp(a, b, g, da, db)
+            def mstep():
+                ops.gemm(a, b, n, n, n, out=c)
+                ops.matmul_vjp(a, b, g, da, db)
 
-        mstep()
-        torch.cuda.synchronize()
-        s0 = torch.cuda.Event(enable_timing=True)
-        s1 = torch.cuda.Event(enable_timing=True)
-        s0.record()
-        for _ in range(args.matmul_steps):
             mstep()
-        s1.record()
-        torch.cuda.synchronize()
-        mms = s0.elapsed_time(s1) / args.matmul_steps
-        mflops = 3 * 2 * n ** 3
-        out["matmul"] = {"n": n, "ms_per_step": round(mms, 4),
-                         "tflops": round(mflops / (mms * 1e-3) / 1e12, 3),
-                         "pct_fp32_mfma_peak": round(100 * mflops / (mms * 1e-3) / 1e12
-                                                     / PEAK_FP32_MFMA_TFLOPS, 2)}
+            torch.cuda.synchronize()
+            gm = capture(mstep)
+            reps = max(1, args.matmul_steps if n >= 2048 else 10 * args.matmul_steps)
+            s0 = torch.cuda.Event(enable_timing=True)
+            s1 = torch.cuda.Event(enable_timing=True)
+            s0.record()
+            for _ in range(reps):
+                gm.replay()
+            s1.record()
+            torch.cuda.synchronize()
+            mms = s0.elapsed_time(s1) / reps
+            mflops = 3 * 2 * n ** 3
+            out["matmul"][str(n)] = {
+                "ms_per_step": round(mms, 4), "steps": reps,
+                "tflops": round(mflops / (mms * 1e-3) / 1e12, 3),
+                "pct_fp32_mfma_peak": round(100 * mflops / (mms * 1e-3) / 1e12
+                                            / PEAK_FP32_MFMA_TFLOPS, 2)}
+            del a, b, g, c, da, db, gm
 
     # The drop-in host-buffer entry points (katsu_amd.host): each pass copies
     # its operands in and its result out over PCIe.  Reported beside `value`,

@@ -33,18 +33,6 @@ __global__ void __launch_bounds__(256) scale_kernel(float *p, int64_t n, float b
         p[i] = (beta == 0.f) ? 0.f : beta * p[i];
 }
 
-// dw = beta*dw + sum_s ws[s][e], s ascending: a fixed order, so the result is
-// the same on every run.
-__global__ void __launch_bounds__(256) dw_reduce_kernel(const float *__restrict__ ws,
-                                                        float *__restrict__ dw, int64_t elems,
-                                                        int splits, float beta) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= elems) return;
-    float acc = 0.f;
-    for (int s = 0; s < splits; ++s) acc += ws[(int64_t)s * elems + e];
-    dw[e] = (beta == 0.f) ? acc : beta * dw[e] + acc;
-}
-
 // ---------------------------------------------------------------------------
 // Library state.
 
@@ -128,6 +116,8 @@ using CfgS = Cfg<16, 256, 16, 16, 64>;   // rows <= 16 (tiny channel counts)
 using CfgM = Cfg<64, 128, 16, 32, 64>;   // rows <= 64
 using CfgL = Cfg<128, 128, 16, 64, 64>;  // large
 using CfgW = Cfg<64, 64, 32, 32, 32>;    // dW: oc x (c,r,s), long split reductions
+using Cfg64 = Cfg<64, 64, 16, 32, 32>;   // mid-size GEMMs (enough tiles for 256 CUs)
+using Cfg32 = Cfg<32, 32, 32, 16, 16>;   // small GEMMs
 
 template <class C, class Prob>
 int run(const Prob &p, int64_t blocks, hipStream_t st) {
@@ -180,10 +170,17 @@ int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_
     if (!c) return KATSU_E_INVALID;
     if (k == 0) return launch_scale(c, (int64_t)m * (int64_t)n, beta, st);
     if (!a || !b) return KATSU_E_INVALID;
-    if (m >= 128 && n >= 128)
+    // The largest tile that still gives every CU a block; tiny row counts
+    // take the 16-row tile.
+    const int64_t M = (int64_t)m, N = (int64_t)n;
+    auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn); };
+    if (m >= 128 && n >= 128 && tiles(128, 128) >= 256)
         return gemm_dispatch<CfgL>(a, b, c, m, n, k, ta, tb, beta, st);
     if (m <= 16) return gemm_dispatch<CfgS>(a, b, c, m, n, k, ta, tb, beta, st);
-    return gemm_dispatch<CfgM>(a, b, c, m, n, k, ta, tb, beta, st);
+    if (m <= 64 && tiles(64, 128) >= 256)
+        return gemm_dispatch<CfgM>(a, b, c, m, n, k, ta, tb, beta, st);
+    if (tiles(64, 64) >= 256) return gemm_dispatch<Cfg64>(a, b, c, m, n, k, ta, tb, beta, st);
+    return gemm_dispatch<Cfg32>(a, b, c, m, n, k, ta, tb, beta, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -386,6 +383,23 @@ struct DirectDwPlan {
 
 constexpr int64_t kDwTargetBlocks = 512;
 
+// Fixed-order sum of split-K partials into dw.  Few elements and many
+// splits: 64 split groups per column so each thread's chain stays short;
+// otherwise 8 groups and more columns per block.
+int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
+                        float beta, hipStream_t st) {
+    if (elems * 4 <= 256LL * 64 && splits >= 64) {
+        constexpr int G = 64;
+        dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
+            ws, dw, elems, pstride, splits, beta);
+    } else {
+        constexpr int G = 8;
+        dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
+            ws, dw, elems, pstride, splits, beta);
+    }
+    return launch_status();
+}
+
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
 bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
@@ -501,12 +515,7 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
         default: return KATSU_E_INVALID;
     }
     if (rc != KATSU_OK || direct) return rc;
-    constexpr int G = 8;
-    const int64_t elems = (int64_t)a.K * a.CRS;
-    const int64_t per_block = (256 / G) * 4;
-    dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, per_block)), dim3(256), 0, st>>>(
-        ws, dw, elems, pl.pstride, pl.splits, beta);
-    return launch_status();
+    return launch_split_reduce(ws, dw, (int64_t)a.K * a.CRS, pl.pstride, pl.splits, beta, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -654,6 +663,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
 
 struct DwPlan {
     int tiles_m, tiles_n, splits, kchunk;
+    int64_t pstride;  // floats between partials (a multiple of 4)
     size_t ws_bytes;
     DirectDwPlan direct;  // used when direct.ok
 };
@@ -675,7 +685,8 @@ DwPlan dw_plan(const ConvDims &d) {
     splits = std::max<int64_t>(1, cdiv(npix, kchunk));
     pl.splits = (int)splits;
     pl.kchunk = (int)kchunk;
-    pl.ws_bytes = splits > 1 ? (size_t)splits * (size_t)d.K * (size_t)d.CRS * sizeof(float) : 0;
+    pl.pstride = ((int64_t)d.K * d.CRS + 3) / 4 * 4;
+    pl.ws_bytes = splits > 1 ? (size_t)splits * (size_t)pl.pstride * sizeof(float) : 0;
     return pl;
 }
 
@@ -722,7 +733,7 @@ int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float 
     p.c.out = direct ? dw : ws;
     p.c.K = d.K;
     p.c.CRS = d.CRS;
-    p.c.split_stride = direct ? 0 : (int64_t)d.K * d.CRS;
+    p.c.split_stride = direct ? 0 : pl.pstride;
     p.c.beta = direct ? beta : 0.f;
     p.c.split = 0;
     p.tiles_m = pl.tiles_m;
@@ -732,10 +743,7 @@ int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float 
     p.npix = (int)d.npix_out;
     int rc = run<C>(p, (int64_t)pl.tiles_m * pl.tiles_n * pl.splits, st);
     if (rc != KATSU_OK || direct) return rc;
-    const int64_t elems = (int64_t)d.K * d.CRS;
-    dw_reduce_kernel<<<dim3((unsigned)cdiv(elems, 256)), dim3(256), 0, st>>>(ws, dw, elems,
-                                                                             pl.splits, beta);
-    return launch_status();
+    return launch_split_reduce(ws, dw, (int64_t)d.K * d.CRS, pl.pstride, pl.splits, beta, st);
 }
 
 int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_conv_geom *g,
