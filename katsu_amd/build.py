@@ -1,7 +1,11 @@
-"""Builds the gfx950 library ``katsu_amd/lib/libkatsu_hip.so`` in-tree.
+"""Builds the native libraries in-tree:
+
+  katsu_amd/lib/libkatsu_hip.so   the gfx950 kernels behind the C ABI (hipcc)
+  katsu_amd/lib/libkatsu.so       the C++ front end (Tensor/Conv2D mirror of
+                                  katsu-core) over that ABI (g++)
 
 hipcc cross-compiles for gfx950 without a GPU, so this runs in the CPU
-container; the resulting .so travels with the tree to the GPU box.
+container; the resulting .so files travel with the tree to the GPU box.
 """
 import os
 import subprocess
@@ -25,6 +29,23 @@ HIP_FLAGS = [
 ]
 
 SOURCES = [os.path.join(CSRC, "katsu_hip.hip")]
+FRONTEND_SRC = os.path.join(HERE, "cpp", "katsu.cpp")
+FRONTEND_LIB = os.path.join(LIB_DIR, "libkatsu.so")
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra"]
+
+
+def build_frontend(verbose: bool = False) -> str:
+    """The C++ front end, linked against libkatsu_hip.so (found next to it)."""
+    tmp = FRONTEND_LIB + ".tmp"
+    cmd = ["g++", *CXX_FLAGS, FRONTEND_SRC, "-o", tmp, "-L", LIB_DIR, "-lkatsu_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, FRONTEND_LIB)
+    return FRONTEND_LIB
 
 
 def build(verbose: bool = False) -> str:
@@ -42,6 +63,7 @@ def build(verbose: bool = False) -> str:
     if err.strip() and verbose:
         print(err, file=sys.stderr)
     os.replace(tmp, LIB)
+    build_frontend(verbose)
     return LIB
 
 

@@ -1,0 +1,192 @@
+// katsu.hpp -- C++ mirror of katsu-core's public API (Tensor, Op, TensorError,
+// Conv2D), whose four kernel seams call the gfx950 library through the C ABI
+// of include/katsu_hip.h.
+//
+// The reference (paths relative to its repository root):
+//   crates/katsu-core/src/lib.rs:4-8       re-exports Tensor, TensorError, Op, Conv2D
+//   crates/katsu-core/src/tensor.rs        Tensor, autograd engine, TensorError
+//   crates/katsu-core/src/conv2d.rs        Conv2D layer, Geometry
+//
+// Names, argument meaning and error behaviour follow the reference.  Rust's
+// `Result<T, TensorError>` becomes katsu::Result<T>; `Rc` handles become
+// shared_ptr handles (a copy shares the node, as `clone()` does); the
+// `RefCell` around a gradient becomes a borrow counter with the same
+// GradientBorrowed failures.  Two names differ because they are C++
+// keywords or conventions: `Tensor::new` is `Tensor::create`, `Conv2D::new`
+// is `Conv2D::create`.
+//
+// The matmul, its VJPs and both convolution passes run on the GPU (host
+// buffers in, host buffers out, as the reference's slices are); the
+// elementwise ops, sum and the graph bookkeeping stay on the host, as in
+// the reference.  A device failure is reported as TensorError::Device, a
+// variant the reference lacks (it has no device).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <string>
+#include <utility>
+#include <variant>
+#include <vector>
+
+namespace katsu {
+
+// tensor.rs:9-30, plus Device for a failed library call.
+struct TensorError {
+    enum class Kind {
+        ShapeOverflow,
+        InvalidConv,
+        MissingForward,
+        NonScalarBackward,
+        GradientBorrowed,
+        DataLength,
+        ShapeMismatch,
+        RankMismatch,
+        MatmulMismatch,
+        Allocation,
+        Device,
+    };
+    Kind kind;
+    const char *message = "";  // InvalidConv
+    size_t a = 0, b = 0;       // DataLength {expected, actual}, RankMismatch {left, right},
+                               // MatmulMismatch {left_columns, right_rows}
+    int status = 0;            // Device: the katsu_status of the failed call
+
+    // The texts of tensor.rs:32-67.
+    std::string to_string() const;
+};
+
+// Result<T, TensorError>: a value or an error.
+template <class T>
+class Result {
+   public:
+    Result(T value) : v_(std::move(value)) {}
+    Result(TensorError e) : v_(std::move(e)) {}
+    bool ok() const { return v_.index() == 0; }
+    explicit operator bool() const { return ok(); }
+    T &value() & { return std::get<0>(v_); }
+    T &&value() && { return std::get<0>(std::move(v_)); }
+    const T &value() const & { return std::get<0>(v_); }
+    const TensorError &error() const { return std::get<1>(v_); }
+    bool is(TensorError::Kind k) const { return !ok() && error().kind == k; }
+
+   private:
+    std::variant<T, TensorError> v_;
+};
+
+struct Unit {};
+using Status = Result<Unit>;
+
+// tensor.rs:84-93.
+struct Op {
+    enum class Kind { Leaf, Add, Mul, Matmul, Conv2D, Sum };
+    Kind kind = Kind::Leaf;
+    size_t stride = 0, padding = 0;  // Conv2D only
+    bool operator==(const Op &o) const {
+        return kind == o.kind && stride == o.stride && padding == o.padding;
+    }
+    bool operator!=(const Op &o) const { return !(*this == o); }
+};
+
+class Tensor;
+struct TensorNode;
+
+// A shared borrow of a node's gradient (Ref<'_, Option<Vec<f32>>>): while it
+// lives, backward and zero_grad on that node fail with GradientBorrowed.
+class GradRef {
+   public:
+    GradRef(const GradRef &) = delete;
+    GradRef &operator=(const GradRef &) = delete;
+    GradRef(GradRef &&o) noexcept : node_(std::exchange(o.node_, nullptr)) {}
+    ~GradRef();
+    // The Option: empty before the first backward reaches this node.
+    const std::optional<std::vector<float>> &operator*() const;
+    const std::optional<std::vector<float>> *operator->() const { return &**this; }
+
+   private:
+    friend class Tensor;
+    explicit GradRef(const TensorNode *n);
+    const TensorNode *node_;
+};
+
+// tensor.rs:95-107: a shared handle; copies preserve node identity.
+class Tensor {
+   public:
+    // Tensor::new (tensor.rs:149-158): takes the data, checks its length.
+    static Result<Tensor> create(std::vector<float> data, const std::vector<size_t> &shape);
+    static Result<Tensor> zeros(const std::vector<size_t> &shape);
+
+    const std::vector<size_t> &shape() const;
+    const std::vector<float> &data() const;
+    size_t rank() const { return shape().size(); }
+    size_t numel() const { return data().size(); }
+    Op op() const;
+    const std::vector<Tensor> &parents() const;
+
+    Result<GradRef> grad() const;
+    Status zero_grad() const;
+
+    Result<Tensor> add(const Tensor &rhs) const;
+    Result<Tensor> mul(const Tensor &rhs) const;
+    Result<Tensor> sum() const;
+    Result<Tensor> matmul(const Tensor &rhs) const;  // seam S1 (GPU)
+
+    Status backward() const;
+    Status backward_with(const std::vector<float> &seed) const;
+
+    bool same_node(const Tensor &o) const { return node_ == o.node_; }
+
+    // Crate-internal (Tensor::node, tensor.rs:182-190).
+    static Tensor node(std::vector<float> data, std::vector<size_t> shape, Op op,
+                       std::vector<Tensor> parents);
+
+   private:
+    explicit Tensor(std::shared_ptr<TensorNode> n) : node_(std::move(n)) {}
+    Result<Tensor> elementwise(const Tensor &rhs, Op::Kind op) const;
+    std::vector<Tensor> topological_order() const;
+    friend struct Engine;
+    std::shared_ptr<TensorNode> node_;
+};
+
+// conv2d.rs:14-20.
+class Conv2D {
+   public:
+    // Conv2D::new (seed 42) and new_seeded (conv2d.rs:22-61).
+    static Result<Conv2D> create(size_t in_channels, size_t out_channels,
+                                 std::pair<size_t, size_t> kernel_size, size_t stride,
+                                 size_t padding);
+    static Result<Conv2D> new_seeded(size_t in_channels, size_t out_channels,
+                                     std::pair<size_t, size_t> kernel_size, size_t stride,
+                                     size_t padding, uint64_t seed);
+    static Result<Conv2D> from_weights(Tensor weights, size_t stride, size_t padding);
+
+    const Tensor &weights() const { return weights_; }
+    size_t in_channels() const { return weights_.shape()[1]; }
+    size_t out_channels() const { return weights_.shape()[0]; }
+    std::pair<size_t, size_t> kernel_size() const {
+        return {weights_.shape()[2], weights_.shape()[3]};
+    }
+    size_t stride() const { return stride_; }
+    size_t padding() const { return padding_; }
+
+    Result<Tensor> forward(const Tensor &input) const;                          // seam S3
+    Result<std::pair<Tensor, Tensor>> backward(const Tensor &grad_output) const;  // seam S4
+    std::optional<Tensor> get_activation_map() const;
+    void clear_cache() const;
+
+   private:
+    Conv2D(Tensor w, size_t stride, size_t padding)
+        : weights_(std::move(w)), stride_(stride), padding_(padding),
+          last_forward_(std::make_shared<std::optional<std::pair<Tensor, Tensor>>>()) {}
+    Tensor weights_;
+    size_t stride_, padding_;
+    // RefCell<Option<(Tensor, Tensor)>>: the last successful forward.
+    std::shared_ptr<std::optional<std::pair<Tensor, Tensor>>> last_forward_;
+};
+
+// tensor.rs:127-138 (crate-internal, exposed for the tests).
+Result<size_t> element_count(const std::vector<size_t> &shape);
+
+}  // namespace katsu

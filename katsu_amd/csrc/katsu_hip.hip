@@ -782,6 +782,12 @@ int h2d(Buffer &b, const float *src, size_t count, hipStream_t st) {
     return map_hip(hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, st));
 }
 
+// beta*C for an empty reduction on a host buffer (beta is 0 or 1).
+int host_scale(float *c, size_t count, float beta) {
+    if (beta == 0.f && count) std::memset(c, 0, count * sizeof(float));
+    return KATSU_OK;
+}
+
 int d2h_sync(float *dst, const Buffer &b, size_t count, hipStream_t st) {
     const size_t bytes = count * sizeof(float);
     if (bytes) {
@@ -850,6 +856,8 @@ int katsu_hip_gemm_f32(const float *a, const float *b, float *c, size_t m, size_
     if (!mul_ok(m, n, (uint64_t *)&mn) || !mul_ok(m, k, (uint64_t *)&mk) ||
         !mul_ok(k, n, (uint64_t *)&kn))
         return KATSU_E_INVALID;
+    // An empty reduction computes nothing: C = beta*C on the caller's buffer.
+    if (k == 0) return host_scale(c, mn, beta);
     State &s = state();
     std::lock_guard<std::mutex> lock(s.mu);
     int rc = init_locked(s);
@@ -956,6 +964,7 @@ int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,
                  ny = (size_t)d.npix_out * d.K;
     if (!dw) return KATSU_E_INVALID;
     if (ny > 0 && (!x || !gy)) return KATSU_E_INVALID;
+    if (ny == 0) return host_scale(dw, nw, beta);  // empty batch: dw = beta*dw
     State &s = state();
     std::lock_guard<std::mutex> lock(s.mu);
     int rc = init_locked(s);

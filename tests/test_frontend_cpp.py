@@ -1,0 +1,86 @@
+"""The reference's 19 integration tests, ported onto the C++ front end
+(katsu_amd/cpp) and run by the driver tests/cpp/_build/test_frontend.
+
+Tests that reach a matmul or convolution kernel need the GPU; the others
+(shape validation, errors, elementwise autograd, empty problems) run
+anywhere.  The driver is run once per session; each test checks its line."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRIVER = os.path.join(ROOT, "tests", "cpp", "_build", "test_frontend")
+
+# No kernel launch: runnable without a GPU.
+HOST_ONLY = [
+    "validates_data_and_storage_size",
+    "scalar_and_empty_shapes",
+    "addition_preserves_inputs",
+    "rejects_invalid_matmul",
+    "empty_matmul_and_output_overflow",
+    "squared_error_shared_nodes_and_repeated_backward",
+    "diamond_and_clone_identity",
+    "explicit_seed_and_errors_are_atomic",
+    "empty_graph_operations",
+    "empty_batch_and_seeded_initialization",
+]
+# Reach the gfx950 kernels through the C ABI.
+DEVICE = [
+    "rectangular_matmul",
+    "matmul_finite_differences",
+    "matmul_same_parent_accumulates_both_edges",
+    "known_forward_and_overlap_gradients",
+    "finite_differences_input_and_weights",
+    "reused_layer_keeps_independent_graphs",
+    "shared_operand_and_chained_convolution",
+    "invalid_shapes_and_overflow",
+    "known_stride_and_padding",
+]
+
+
+def _driver():
+    if not os.path.exists(DRIVER):
+        sys.path.insert(0, os.path.join(ROOT, "tests", "cpp"))
+        import build as cpp_build  # noqa: E402
+        cpp_build.build()
+    return DRIVER
+
+
+def _run(names):
+    proc = subprocess.run([_driver(), *names], capture_output=True, text=True, timeout=600)
+    results = {}
+    for line in proc.stdout.splitlines():
+        status, _, rest = line.partition(" ")
+        name = rest.split(":", 1)[0]
+        results[name] = (status, line)
+    return results
+
+
+@pytest.fixture(scope="module")
+def host_results():
+    return _run(HOST_ONLY)
+
+
+@pytest.fixture(scope="module")
+def device_results():
+    return _run(DEVICE)
+
+
+def test_every_reference_test_is_ported():
+    assert len(HOST_ONLY) + len(DEVICE) == 19
+    assert not set(HOST_ONLY) & set(DEVICE)
+
+
+@pytest.mark.parametrize("name", HOST_ONLY)
+def test_frontend_host(name, host_results):
+    status, line = host_results.get(name, ("MISSING", name))
+    assert status == "PASS", line
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", DEVICE)
+def test_frontend_device(name, device_results):
+    status, line = device_results.get(name, ("MISSING", name))
+    assert status == "PASS", line
