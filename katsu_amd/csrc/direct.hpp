@@ -389,6 +389,9 @@ struct DirectDwArgs {
     int tiles_img, tiles_total, tiles_per_split;
     int k_blocks, c_blocks;
     int ncols;
+    int gpitch;          // LDS row pitch of the G tile, == 2 (mod 4), >= gcap
+    int gcap;            // G floats staged per row: trows*seg_w rounded up to 4
+    int stage;           // floats per LDS stage: KT*gpitch + CT*CPITCH
     int g_vec;           // 1: tile starts and OHW are multiples of 4 (16-byte G rows)
     int out_vec;         // 1: partial rows are 16-byte aligned runs
     int64_t split_stride;  // floats between partials, or 0 when writing dw directly
@@ -396,29 +399,33 @@ struct DirectDwArgs {
     FastDiv fd_tiles_img, fd_segs;
 };
 
+// Compile-time part of the dW LDS layout; the G tile's pitch is chosen per
+// problem (the tightest pitch == 2 mod 4, which keeps the A reads of a
+// half-wave on 32 distinct banks).
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
 struct DirectDwGeo {
     static constexpr int PITCH = 64 * CC;
     static constexpr int CPITCH = ROWS * PITCH + 2;   // == 2 (mod 32)
-    static constexpr int GPITCH = 64 * GPC + 2;       // == 2 (mod 32)
-    static constexpr int GS = KT * GPITCH;
-    static constexpr int STAGE = GS + CT * CPITCH;
+    static constexpr int XS = CT * CPITCH;
     static constexpr int PPITCH = CT * R * S + 4;     // partial transpose buffer
-    static_assert(KT * PPITCH <= 2 * STAGE, "partial tile must fit the LDS stages");
-    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+    static constexpr int GMAX = 64 * GPC;             // G floats per row, at most
 };
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
+// WKF: 16-row output-channel fragments per wave.  A wave owns
+// (16*WKF) oc x 16 c x R*S taps; each k-step reads WKF A and R*S B
+// fragments for WKF*R*S MFMAs.  FULL: every tile row is a multiple of 4
+// pixels wide, so no k-step holds a pixel past the end of its row.
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
 __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
     constexpr int RS = R * S;
-    constexpr int WK = KT / 16;         // waves along output channels
-    constexpr int CPW = CT / 4;         // input channels staged per wave
-    constexpr int GRW = KT / 4;         // G rows staged per wave (scalar path)
-    constexpr int G4 = 16 * GPC;        // float4 per G tile row, at most
-    constexpr int GQ4 = KT * G4 / 256;  // float4 G loads per thread
-    static_assert(KT % 16 == 0 && CT % 16 == 0 && (KT / 16) * (CT / 16) == 4,
-                  "4 waves of 16x16 slices");
+    constexpr int WK = KT / (16 * WKF);  // waves along output channels
+    constexpr int CPW = CT / 4;          // input channels staged per wave
+    constexpr int GRW = KT / 4;          // G rows staged per wave (scalar path)
+    constexpr int G4 = 16 * GPC;         // float4 per G tile row, at most
+    constexpr int GQ4 = KT * G4 / 256;   // float4 G loads per thread
+    static_assert(KT % (16 * WKF) == 0 && CT % 16 == 0 && WK * (CT / 16) == 4,
+                  "4 waves of (16*WKF) x 16 slices");
     static_assert((KT * G4) % 256 == 0, "G tile must split evenly over the block");
 
     extern __shared__ float smem[];
@@ -434,6 +441,7 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     const int k0 = kb * KT, c0 = cb * CT;
     const int tb = split * a.tiles_per_split;
     const int te = min(tb + a.tiles_per_split, a.tiles_total);
+    const int gs_floats = KT * a.gpitch;  // the G part of a stage
 
     int colb[CC];
 #pragma unroll
@@ -510,18 +518,21 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
             for (int q = 0; q < GQ4; ++q) {
                 const int e4 = q * 256 + tid;
                 const int row = e4 / G4, c4 = e4 % G4;
-                float *d = base + row * Geo::GPITCH + c4 * 4;  // 8-byte aligned
-                *reinterpret_cast<float2 *>(d) = make_float2(gr4[q][0], gr4[q][1]);
-                *reinterpret_cast<float2 *>(d + 2) = make_float2(gr4[q][2], gr4[q][3]);
+                if (c4 * 4 < a.gcap) {
+                    float *d = base + row * a.gpitch + c4 * 4;  // 8-byte aligned
+                    *reinterpret_cast<float2 *>(d) = make_float2(gr4[q][0], gr4[q][1]);
+                    *reinterpret_cast<float2 *>(d + 2) = make_float2(gr4[q][2], gr4[q][3]);
+                }
             }
         } else {
-            float *gs = base + wave * Geo::GPITCH + lane;
+            float *gs = base + wave * a.gpitch + lane;
 #pragma unroll
             for (int i = 0; i < GRW; ++i)
 #pragma unroll
-                for (int c = 0; c < GPC; ++c) gs[4 * i * Geo::GPITCH + c * 64] = gr[i * GPC + c];
+                for (int c = 0; c < GPC; ++c)
+                    if (lane + c * 64 < a.gcap) gs[4 * i * a.gpitch + c * 64] = gr[i * GPC + c];
         }
-        float *xs = base + Geo::GS + wave * Geo::CPITCH + lane;
+        float *xs = base + gs_floats + wave * Geo::CPITCH + lane;
 #pragma unroll
         for (int j = 0; j < CPW; ++j)
 #pragma unroll
@@ -531,31 +542,37 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
                     xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
     };
 
-    floatx4 acc[RS];
+    floatx4 acc[WKF][RS];
 #pragma unroll
-    for (int i = 0; i < RS; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < WKF; ++f)
+#pragma unroll
+        for (int i = 0; i < RS; ++i) acc[f][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int arow = (wk * 16 + (lane & 15)) * Geo::GPITCH;
-    const int bch = Geo::GS + (wc * 16 + (lane & 15)) * Geo::CPITCH;
+    const int arow = (wk * 16 * WKF + (lane & 15)) * a.gpitch;
+    const int bch = gs_floats + (wc * 16 + (lane & 15)) * Geo::CPITCH;
     const int lq = lane >> 4;  // the lane's pixel within a k-step
 
     // One stage: k-steps over (tile row, 4-column group), two register sets
-    // so the fragments of step s+1 are read while step s's MFMAs run.  A lane
-    // past the end of its tile row reads the row's last pixel (finite data)
-    // and its G value is zeroed at MFMA time, so it contributes nothing; the
-    // mask is applied after the next step's reads are issued, keeping the
-    // LDS latency off the MFMA path.
+    // so the fragments of step s+1 are read while step s's MFMAs run.  With
+    // FULL every lane's pixel is valid and its addresses are a per-lane base
+    // plus a uniform step offset.  Otherwise a lane past the end of its tile row reads the
+    // row's last pixel (finite data) and its G values are zeroed at MFMA time,
+    // so it contributes nothing; the mask is applied after the next step's
+    // reads are issued, keeping the LDS latency off the MFMA path.
     auto compute = [&](const float *base, const TileGeo &tg) __attribute__((always_inline)) {
         const int wseg = tg.cx1 - tg.cx0;
         const int cpr = (wseg + 3) >> 2;
         const int nsteps = tg.tr * cpr;
         int fr = 0, fc = 0;  // (tile row, column group) of the next step to fetch
-        auto fetch = [&](float &av, float (&b)[RS], bool &ok) __attribute__((always_inline)) {
+        auto fetch = [&](float (&av)[WKF], float (&b)[RS], bool &ok)
+            __attribute__((always_inline)) {
             const int row = min(fr, tg.tr - 1);  // a fetch past the last step re-reads it
             const int col = tg.cx0 + fc * 4 + lq;
-            ok = col < tg.cx1;
-            const int cc = min(col, tg.cx1 - 1);
-            av = base[arow + row * wseg + (cc - tg.cx0)];
+            ok = FULL || col < tg.cx1;
+            const int cc = FULL ? col : min(col, tg.cx1 - 1);
+            const float *gsrc = base + arow + row * wseg + (cc - tg.cx0);
+#pragma unroll
+            for (int f = 0; f < WKF; ++f) av[f] = gsrc[f * 16 * a.gpitch];
             const float *xs = base + bch + row * a.st * Geo::PITCH + cc * a.st;
 #pragma unroll
             for (int tap = 0; tap < RS; ++tap) b[tap] = xs[(tap / S) * Geo::PITCH + tap % S];
@@ -564,31 +581,34 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
                 ++fr;
             }
         };
-        auto mma = [&](const float av, const float (&b)[RS], const bool ok)
+        auto mma = [&](const float (&av)[WKF], const float (&b)[RS], const bool ok)
             __attribute__((always_inline)) {
-            const float am = ok ? av : 0.f;
 #pragma unroll
-            for (int tap = 0; tap < RS; ++tap)
-                acc[tap] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, b[tap], acc[tap], 0, 0, 0);
+            for (int f = 0; f < WKF; ++f) {
+                const float am = FULL || ok ? av[f] : 0.f;
+#pragma unroll
+                for (int tap = 0; tap < RS; ++tap)
+                    acc[f][tap] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(am, b[tap], acc[f][tap], 0, 0, 0);
+            }
         };
-        float a0, a1, b0[RS], b1[RS];
+        float a0[WKF], a1[WKF], b0[RS], b1[RS];
         bool k0ok, k1ok;
         fetch(a0, b0, k0ok);
         asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
         for (int s = 0; s < nsteps; s += 2) {
             fetch(a1, b1, k1ok);
             mma(a0, b0, k0ok);
-            order_reads_then_mfma<RS + 1, RS>();
+            order_reads_then_mfma<WKF + RS, WKF * RS>();
             if (s + 1 >= nsteps) break;
             fetch(a0, b0, k0ok);
             mma(a1, b1, k1ok);
-            order_reads_then_mfma<RS + 1, RS>();
+            order_reads_then_mfma<WKF + RS, WKF * RS>();
         }
     };
-
     if (tb < te) {
         float *st0 = smem;
-        float *st1 = smem + Geo::STAGE;
+        float *st1 = smem + a.stage;
         TileGeo cur = geo(tb);
         load(cur);
         store(st0);
@@ -620,11 +640,13 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     // CT*RS floats per output channel.
     float *ps = smem;
 #pragma unroll
-    for (int tap = 0; tap < RS; ++tap)
+    for (int f = 0; f < WKF; ++f)
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            ps[(wk * 16 + 4 * (lane >> 4) + v) * Geo::PPITCH + (wc * 16 + (lane & 15)) * RS + tap] =
-                acc[tap][v];
+        for (int tap = 0; tap < RS; ++tap)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ps[(wk * 16 * WKF + f * 16 + 4 * (lane >> 4) + v) * Geo::PPITCH +
+                   (wc * 16 + (lane & 15)) * RS + tap] = acc[f][tap][v];
     __syncthreads();
     float *ob = a.out + (int64_t)split * a.split_stride;
     const int len = min(CT, a.C - c0) * RS;  // valid floats of a row
@@ -666,12 +688,26 @@ __global__ void __launch_bounds__(256) dw_split_reduce(const float *__restrict__
     const int64_t e = ((int64_t)blockIdx.x * E4 + col) * 4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (e + 3 < elems) {
-        for (int k = grp; k < splits; k += G) {
-            const float4 v = *reinterpret_cast<const float4 *>(part + (int64_t)k * pstride + e);
-            s.x += v.x;
-            s.y += v.y;
-            s.z += v.z;
-            s.w += v.w;
+        // Eight loads in flight per thread, then added in split order.
+        constexpr int U = 8;
+        for (int k0 = grp; k0 < splits; k0 += U * G) {
+            float4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = k0 + u * G;
+                v[u] = k < splits
+                    ? *reinterpret_cast<const float4 *>(part + (int64_t)k * pstride + e)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (k0 + u * G < splits) {
+                    s.x += v[u].x;
+                    s.y += v[u].y;
+                    s.z += v[u].z;
+                    s.w += v[u].w;
+                }
+            }
         }
     } else if (e < elems) {
         for (int k = grp; k < splits; k += G) {

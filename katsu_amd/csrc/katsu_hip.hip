@@ -379,33 +379,35 @@ struct DirectDwPlan {
     int splits = 0;
     int64_t pstride = 0;  // floats between partials
     size_t ws_bytes = 0;
+    size_t lds_bytes = 0;
+    bool full = false;  // every tile row is a multiple of 4 pixels wide
 };
 
-constexpr int64_t kDwTargetBlocks = 512;
-
-// Fixed-order sum of split-K partials into dw.  Few elements and many
-// splits: 64 split groups per column so each thread's chain stays short;
-// otherwise 8 groups and more columns per block.
-int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
-                        float beta, hipStream_t st) {
-    if (elems * 4 <= 256LL * 64 && splits >= 64) {
-        constexpr int G = 64;
-        dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
-            ws, dw, elems, pstride, splits, beta);
-    } else {
-        constexpr int G = 8;
-        dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
-            ws, dw, elems, pstride, splits, beta);
-    }
+// Fixed-order sum of split-K partials into dw.  G split groups per float4
+// column: the smallest power of two in [8, 64] that keeps each thread's
+// chain at 8 loads or fewer, so the partials stream with many loads in flight.
+template <int G>
+int split_reduce_g(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
+                   float beta, hipStream_t st) {
+    dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
+        ws, dw, elems, pstride, splits, beta);
     return launch_status();
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
+int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
+                        float beta, hipStream_t st) {
+    const int64_t chain = cdiv(splits, 8);
+    if (chain <= 8) return split_reduce_g<8>(ws, dw, elems, pstride, splits, beta, st);
+    if (chain <= 16) return split_reduce_g<16>(ws, dw, elems, pstride, splits, beta, st);
+    if (chain <= 32) return split_reduce_g<32>(ws, dw, elems, pstride, splits, beta, st);
+    return split_reduce_g<64>(ws, dw, elems, pstride, splits, beta, st);
+}
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, int TB>
 bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
-    static_assert(Geo::kBytes <= kLdsMax, "LDS");
     if (d.R != R || d.S != S) return false;
-    const int64_t tmax = 64 * GPC;  // G tile capacity (pixels)
+    const int64_t tmax = Geo::GMAX;  // G tile capacity (pixels)
     const int64_t ncols = (int64_t)(d.OW - 1) * d.st + S;
     if (ncols > 64 * CC || R > ROWS) return false;
     // Buffer resources address one image of x and of G in bytes.
@@ -419,11 +421,18 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     } else {
         seg_w = cdiv(d.OW, cdiv(d.OW, tmax));
     }
+    // LDS: two stages of [KT][gpitch] G + [CT][CPITCH] x; the epilogue's
+    // [KT][PPITCH] transpose reuses them.
+    const int64_t gcap = (trows * seg_w + 3) / 4 * 4;
+    const int64_t gpitch = gcap % 4 == 0 ? gcap + 2 : gcap;  // == 2 (mod 4)
+    const int64_t stage = KT * gpitch + Geo::XS;
+    const int64_t lds = std::max<int64_t>(2 * stage, (int64_t)KT * Geo::PPITCH) * 4;
+    if (lds > kLdsMax) return false;
     const int64_t segs = cdiv(d.OW, seg_w);
     const int64_t tiles_img = cdiv(d.OH, trows) * segs;
     const int64_t tiles_total = (int64_t)d.N * tiles_img;
     const int64_t kb = cdiv(d.K, KT), cb = cdiv(d.C, CT);
-    int64_t splits = std::max<int64_t>(1, cdiv(kDwTargetBlocks, kb * cb));
+    int64_t splits = std::max<int64_t>(1, cdiv(TB, kb * cb));
     splits = std::min(splits, tiles_total);
     const int64_t tps = cdiv(tiles_total, splits);
     splits = cdiv(tiles_total, tps);
@@ -457,6 +466,9 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     a.k_blocks = (int)kb;
     a.c_blocks = (int)cb;
     a.ncols = (int)ncols;
+    a.gpitch = (int)gpitch;
+    a.gcap = (int)gcap;
+    a.stage = (int)stage;
     // 16-byte G rows need every tile start (a multiple of trows*OW, or of
     // seg_w within a row) and OHW to be multiples of 4; pointer alignment is
     // checked at launch.
@@ -469,23 +481,41 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     pl->ok = true;
     pl->blocks = blocks;
     pl->splits = (int)splits;
+    pl->lds_bytes = (size_t)lds;
+    pl->full = segs == 1 ? d.OW % 4 == 0
+                         : seg_w % 4 == 0 && (d.OW - (segs - 1) * seg_w) % 4 == 0;
     pl->pstride = (elems + 3) / 4 * 4;
     pl->ws_bytes = splits > 1 ? (size_t)splits * (size_t)pl->pstride * sizeof(float) : 0;
     return true;
 }
 
-// Variant table: the planner and the kernel of each direct dW variant.
-#define KATSU_DW_VARIANTS(X) X(0, 64, 16, 3, 3, 3, 1, 1)
+// Variant table: id, block tile (KT output x CT input channels), filter
+// R x S, halo rows and column chunks of the x tile, G tile capacity in
+// 64-pixel chunks, oc fragments per wave, and the target block count that
+// sets the split over output pixels.
+#ifndef KATSU_DW_VARIANTS
+#define KATSU_DW_VARIANTS(X) X(0, 64, 32, 3, 3, 3, 1, 1, 2, 512)
+#endif
 
 DirectDwPlan direct_dw_plan_any(const ConvDims &d) {
     DirectDwPlan pl;
-#define KATSU_DW_TRY(id, KT, CT, R, S, ROWS, CC, GPC)                                  \
-    if (pl.variant < 0 && d.K >= KT && direct_dw_plan<KT, CT, R, S, ROWS, CC, GPC>(d, &pl)) \
+#define KATSU_DW_TRY(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)                        \
+    if (pl.variant < 0 && d.K >= KT &&                                                \
+        direct_dw_plan<KT, CT, R, S, ROWS, CC, GPC, WKF, TB>(d, &pl))                 \
         pl.variant = id;
     KATSU_DW_VARIANTS(KATSU_DW_TRY)
 #undef KATSU_DW_TRY
     pl.ok = pl.variant >= 0;
     return pl;
+}
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
+int dw_kernel_launch(const DirectDwPlan &pl, hipStream_t st) {
+    constexpr auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>;
+    const int rc = lds_optin<kern>(kLdsMax);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3((unsigned)pl.blocks), dim3(256), pl.lds_bytes, st>>>(pl.a);
+    return launch_status();
 }
 
 int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw, float beta,
@@ -501,15 +531,11 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
     if (!aligned16(a.out)) a.out_vec = 0;
     int rc = KATSU_E_INVALID;
     switch (pl.variant) {
-#define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC)                                   \
-    case id: {                                                                       \
-        using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;                        \
-        constexpr auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC>;         \
-        if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;              \
-        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a);          \
-        rc = launch_status();                                                        \
-        break;                                                                       \
-    }
+#define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)                      \
+    case id:                                                                         \
+        rc = pl.full ? dw_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true>(pl, st)  \
+                     : dw_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false>(pl, st); \
+        break;
         KATSU_DW_VARIANTS(KATSU_DW_CASE)
 #undef KATSU_DW_CASE
         default: return KATSU_E_INVALID;
