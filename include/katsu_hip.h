@@ -119,6 +119,18 @@ int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *
                                         void *workspace, size_t workspace_bytes,
                                         void *stream);
 
+/* Both passes of backward_buffers (conv2d.rs:265-292) in one call:
+ * dx = beta*dx + dX and dw = beta*dw + dW, as the two calls above make them
+ * (same results, same determinism).  When both passes take their direct
+ * gfx950 kernels they share one launch, so dW work fills the GPU while the
+ * last dX tiles finish.  The _dev form takes the workspace of
+ * katsu_hip_conv2d_bwd_filter_workspace (or NULL, as above). */
+int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
+                             float *dw, const katsu_conv_geom *g, float beta);
+int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy, float *dx,
+                                 float *dw, const katsu_conv_geom *g, float beta,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@ EXPORTS = (
     "katsu_hip_conv2d_bwd_data_f32", "katsu_hip_conv2d_bwd_data_f32_dev",
     "katsu_hip_conv2d_bwd_filter_workspace",
     "katsu_hip_conv2d_bwd_filter_f32", "katsu_hip_conv2d_bwd_filter_f32_dev",
+    "katsu_hip_conv2d_bwd_f32", "katsu_hip_conv2d_bwd_f32_dev",
 )
 
 
@@ -65,6 +66,8 @@ def lib():
         L.katsu_hip_conv2d_bwd_filter_workspace.argtypes = [gp, ctypes.POINTER(sz)]
         L.katsu_hip_conv2d_bwd_filter_f32.argtypes = [vp, vp, vp, gp, fp]
         L.katsu_hip_conv2d_bwd_filter_f32_dev.argtypes = [vp, vp, vp, gp, fp, vp, sz, vp]
+        L.katsu_hip_conv2d_bwd_f32.argtypes = [vp, vp, vp, vp, vp, gp, fp]
+        L.katsu_hip_conv2d_bwd_f32_dev.argtypes = [vp, vp, vp, vp, vp, gp, fp, vp, sz, vp]
         for name in EXPORTS:
             if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown"):
                 getattr(L, name).restype = i

@@ -376,7 +376,7 @@ Result<katsu_conv_geom> geometry(const Tensor &input, const Tensor &weights, siz
 }
 
 // backward_buffers, conv2d.rs:269-292, seam S4: fresh dx and dw, both from
-// the GPU (beta = 0).
+// the GPU in one call (beta = 0).
 Result<std::pair<std::vector<float>, std::vector<float>>> backward_buffers(
     const Tensor &input, const Tensor &weights, const std::vector<float> &grad, size_t stride,
     size_t padding) {
@@ -385,13 +385,8 @@ Result<std::pair<std::vector<float>, std::vector<float>>> backward_buffers(
     if (grad.size() != expected) return data_length(expected, grad.size());
     KATSU_TRY(dx, zeros_buffer(input.numel()));
     KATSU_TRY(dw, zeros_buffer(weights.numel()));
-    if (!dx.empty()) {
-        const int rc = katsu_hip_conv2d_bwd_data_f32(grad.data(), weights.data().data(),
-                                                     dx.data(), &g, 0.0f);
-        if (rc != KATSU_OK) return device(rc);
-    }
-    const int rc = katsu_hip_conv2d_bwd_filter_f32(input.data().data(), grad.data(), dw.data(),
-                                                   &g, 0.0f);
+    const int rc = katsu_hip_conv2d_bwd_f32(input.data().data(), weights.data().data(),
+                                            grad.data(), dx.data(), dw.data(), &g, 0.0f);
     if (rc != KATSU_OK) return device(rc);
     return std::make_pair(std::move(dx), std::move(dw));
 }

@@ -67,6 +67,20 @@ __device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) 
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// LDS-direct buffer loads: lane l's 4 (or 16) bytes land at dst + 4*l (or
+// 16*l) without passing through registers; an out-of-range lane writes zeros.
+// dst must be uniform across the wave.  Completion is tracked by vmcnt, so a
+// stage written this way is waited for with wait_lds_dma() before the barrier
+// that publishes it.
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void lds_dma_b32(__amdgpu_buffer_rsrc_t r, float *dst, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 4, off, 0, 0, 0);
+}
+__device__ __forceinline__ void lds_dma_b128(__amdgpu_buffer_rsrc_t r, float *dst, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ---------------------------------------------------------------------------
 // Forward / data-gradient kernel.
 //
@@ -100,12 +114,15 @@ struct DirectFwdGeo {
     static constexpr int CPITCH = ROWS * PITCH + 16;    // channel pitch, == 16 (mod 32)
     static constexpr int XS = CB * CPITCH;              // input tile
     // Weight tile, kept in the global order of its rows:
-    //   WMODE 0: KT rows (co) of CB*RS floats, pitch CB*RS + 1
+    //   WMODE 0: KT rows (co) of CB*RS floats, pitch CB*RS + 4
     //   WMODE 1: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
+    // Pitches are multiples of 4 floats so 16-byte DMA lands on row
+    // boundaries; the region is a whole number of 256-float wave loads.
     static constexpr int WROWS = WMODE == 0 ? KT : CB;
     static constexpr int WLEN = WMODE == 0 ? CB * RS : KT * RS;
-    static constexpr int WPITCH = WMODE == 0 ? WLEN + 1 : WLEN + ((16 - WLEN % 32) + 32) % 32;
-    static constexpr int WS = WROWS * WPITCH;
+    static constexpr int WPITCH = WMODE == 0 ? WLEN + 4 : WLEN + ((16 - WLEN % 32) + 32) % 32;
+    static constexpr int WS = (WROWS * WPITCH + 255) / 256 * 256;
+    static_assert(WLEN % 4 == 0 && WPITCH % 4 == 0, "weight rows of whole float4");
     static constexpr int STAGE = XS + WS;
     // Output transpose buffer (reuses the stages after the last chunk).
     static constexpr int TPMAX = (4 / (KT / 16)) * F * 16;  // pixels per tile, at most
@@ -114,27 +131,23 @@ struct DirectFwdGeo {
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
 };
 
+// Block `bid` of `nb` (the kernel below, or the dX half of the fused
+// backward launch).
 template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE, bool WVEC>
-__global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
+__device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
     constexpr int RS = R * S;
     constexpr int WOC = KT / 16;            // waves along output channels
     constexpr int CPW = CB / 4;             // input channels staged per wave
-    // Weight staging: scalar (TPR threads per row) or 16-byte (float4 per lane).
-    constexpr int TPR = 256 / Geo::WROWS;
-    constexpr int WPT = (Geo::WLEN + TPR - 1) / TPR;
-    constexpr int W4ROW = Geo::WLEN / 4;                       // float4 per row
-    constexpr int WQ4 = (Geo::WROWS * W4ROW + 255) / 256;      // float4 per thread
     static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
-    static_assert(CB % 4 == 0 && 256 % Geo::WROWS == 0, "CB must be a multiple of 4");
-    static_assert(!WVEC || Geo::WLEN % 4 == 0, "16-byte weight rows");
+    static_assert(CB % 4 == 0, "CB must be a multiple of 4");
 
     extern __shared__ float smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int woc = wave % WOC, wpx = wave / WOC;
 
-    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int t = xcd_swizzle(bid, nb);
     const int cob = t % a.co_blocks;
     const int rest = t / a.co_blocks;
     const int n = rest / a.tiles_img;
@@ -159,8 +172,11 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
         ? (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS
         : (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS;
 
-    // ---- staging: input halo rows ------------------------------------------
-    // Wave w stages channels w + 4j (j < CPW), every row, 64 columns per chunk.
+    // ---- staging: LDS-direct loads ------------------------------------------
+    // Input halo: wave w stages channels w + 4j (j < CPW), one 64-column
+    // row chunk per load.  Weights: 16-byte loads when every float4 of a row
+    // lies inside the row (WVEC), else 4-byte loads.  Padding, rows past the
+    // image and channels past the count read as zeros.
     const __amdgpu_buffer_rsrc_t rin =
         buf_rsrc(a.in + (int64_t)n * a.in_img, (uint32_t)(a.in_img * 4));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, a.w_bytes);
@@ -171,17 +187,12 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
         const int ix = col - a.padx;
         colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
-    float xr[CPW][ROWS][CC];
+    const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform wave index
 
-    // ---- staging: weights ----------------------------------------------------
-    const int wrow = tid / TPR, wcol = tid % TPR;
-    float wr[WVEC ? 1 : WPT];
-    floatx4 wr4[WVEC ? WQ4 : 1];
-
-    auto load = [&](int ci0) __attribute__((always_inline)) {
+    auto stage_in = [&](float *stage, int ci0) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
-            const int ci = ci0 + wave + 4 * j;
+            const int ci = ci0 + wv + 4 * j;
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 const int iy = iy0 + r;
@@ -189,78 +200,48 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
                 const int rowb = (ci * a.H + iy) * a.W * 4;
 #pragma unroll
                 for (int c = 0; c < CC; ++c)
-                    xr[j][r][c] = buf_load(rin, rok ? rowb + colb[c] : kOOB);
+                    lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * Geo::PITCH + c * 64,
+                                rok ? rowb + colb[c] : kOOB);
             }
         }
-        if (WVEC) {
-            // Flat float4 index over WROWS rows of WLEN floats; lim = valid
-            // floats of a row (partial last chunk, channels past the count).
-#pragma unroll
-            for (int q = 0; q < WQ4; ++q) {
-                const int e4 = q * 256 + tid;
-                const int row = e4 / W4ROW, c4 = e4 - (e4 / W4ROW) * W4ROW;
-                int off = kOOB;
-                if (WMODE == 0) {
-                    const int co = co0 + row;
-                    const int lim = min(CB, a.CI - ci0) * RS;
-                    if (row < KT && co < a.CO && c4 * 4 < lim)
-                        off = (((co * a.CI + ci0) * RS) + c4 * 4) * 4;
-                } else {
-                    const int ci = ci0 + row;
-                    const int lim = min(KT, a.CO - co0) * RS;
-                    if (row < CB && ci < a.CI && c4 * 4 < lim)
-                        off = (((ci * a.CO + co0) * RS) + c4 * 4) * 4;
-                }
-                wr4[q] = buf_load4(rw, off);
-            }
-        } else {
-            int rowb, lim;
+        // Valid floats of a weight row in this chunk, and its global start.
+        float *wst = stage + Geo::XS;
+        auto woff = [&](int row, int col) __attribute__((always_inline)) {
             if (WMODE == 0) {
-                // row co = co0 + wrow: CB*RS contiguous floats from w[co][ci0][0][0].
-                const int co = co0 + wrow;
-                lim = co < a.CO ? min(CB, a.CI - ci0) * RS : 0;
-                rowb = (co * a.CI + ci0) * RS * 4;
+                const int co = co0 + row;
+                const int lim = min(CB, a.CI - ci0) * RS;
+                return (row < KT && co < a.CO && col < lim) ? ((co * a.CI + ci0) * RS + col) * 4
+                                                            : kOOB;
             } else {
-                // row ci = ci0 + wrow: KT*RS contiguous floats from w[ci][co0][0][0].
-                const int ci = ci0 + wrow;
-                lim = ci < a.CI ? min(KT, a.CO - co0) * RS : 0;
-                rowb = (ci * a.CO + co0) * RS * 4;
+                const int ci = ci0 + row;
+                const int lim = min(KT, a.CO - co0) * RS;
+                return (row < CB && ci < a.CI && col < lim) ? ((ci * a.CO + co0) * RS + col) * 4
+                                                            : kOOB;
             }
-#pragma unroll
-            for (int q = 0; q < WPT; ++q) {
-                const int e = wcol + TPR * q;
-                wr[q] = buf_load(rw, (e < lim && e < Geo::WLEN) ? rowb + e * 4 : kOOB);
-            }
-        }
-    };
-
-    auto store = [&](float *base) __attribute__((always_inline)) {
-        float *xs = base + wave * Geo::CPITCH + lane;
-#pragma unroll
-        for (int j = 0; j < CPW; ++j)
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-                for (int c = 0; c < CC; ++c)
-                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
+        };
         if (WVEC) {
+            constexpr int NI = Geo::WS / 256;  // wave loads of 64 float4
+            constexpr int W4P = Geo::WPITCH / 4;
 #pragma unroll
-            for (int q = 0; q < WQ4; ++q) {
-                const int e4 = q * 256 + tid;
-                const int row = e4 / W4ROW, c4 = e4 - (e4 / W4ROW) * W4ROW;
-                if (row < Geo::WROWS) {
-                    float *d = base + Geo::XS + row * Geo::WPITCH + c4 * 4;
-                    d[0] = wr4[q][0];
-                    d[1] = wr4[q][1];
-                    d[2] = wr4[q][2];
-                    d[3] = wr4[q][3];
+            for (int q = 0; q < (NI + 3) / 4; ++q) {
+                const int i = q * 4 + wv;
+                if (i < NI) {
+                    const int e4 = i * 64 + lane;
+                    const int row = e4 / W4P, c4 = e4 - (e4 / W4P) * W4P;
+                    lds_dma_b128(rw, wst + i * 256, woff(row, c4 * 4));
                 }
             }
         } else {
-            float *ws = base + Geo::XS + wrow * Geo::WPITCH + wcol;
+            constexpr int NI = Geo::WS / 64;  // wave loads of 64 floats
 #pragma unroll
-            for (int q = 0; q < WPT; ++q)
-                if (wcol + TPR * q < Geo::WLEN) ws[TPR * q] = wr[q];
+            for (int q = 0; q < (NI + 3) / 4; ++q) {
+                const int i = q * 4 + wv;
+                if (i < NI) {
+                    const int e = i * 64 + lane;
+                    const int row = e / Geo::WPITCH, col = e - (e / Geo::WPITCH) * Geo::WPITCH;
+                    lds_dma_b32(rw, wst + i * 64, woff(row, col));
+                }
+            }
         }
     };
 
@@ -305,23 +286,23 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
     };
 
     // Two-stage pipeline: while chunk ch is consumed from one stage, chunk
-    // ch+1 is fetched into registers and written to the other stage.  The
-    // loop is unrolled by two so each stage's base is a constant.
+    // ch+1 streams into the other.  The loop is unrolled by two so each
+    // stage's base is a constant.
     const int nch = (a.CI + CB - 1) / CB;
     float *st0 = smem;
     float *st1 = smem + Geo::STAGE;
-    load(0);
-    store(st0);
+    stage_in(st0, 0);
+    wait_lds_dma();
     __syncthreads();
     for (int ch = 0; ch < nch; ch += 2) {
-        if (ch + 1 < nch) load((ch + 1) * CB);
+        if (ch + 1 < nch) stage_in(st1, (ch + 1) * CB);
         compute(st0);
-        if (ch + 1 < nch) store(st1);
+        wait_lds_dma();
         __syncthreads();
         if (ch + 1 >= nch) break;
-        if (ch + 2 < nch) load((ch + 2) * CB);
+        if (ch + 2 < nch) stage_in(st0, (ch + 2) * CB);
         compute(st1);
-        if (ch + 2 < nch) store(st0);
+        wait_lds_dma();
         __syncthreads();
     }
 
@@ -360,6 +341,11 @@ __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) 
                 store_beta(dst + p, ys[row * Geo::YPITCH + p], a.beta);
         }
     }
+}
+
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE, bool WVEC>
+__global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
+    direct_fwd_block<KT, F, CB, R, S, ROWS, CC, WMODE, WVEC>(a, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -416,7 +402,7 @@ struct DirectDwGeo {
 // fragments for WKF*R*S MFMAs.  FULL: every tile row is a multiple of 4
 // pixels wide, so no k-step holds a pixel past the end of its row.
 template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
-__global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
+__device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, int nb) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
     constexpr int RS = R * S;
     constexpr int WK = KT / (16 * WKF);  // waves along output channels
@@ -433,7 +419,7 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wk = wave % WK, wc = wave / WK;
 
-    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int t = xcd_swizzle(bid, nb);
     const int kb = t % a.k_blocks;
     const int rest = t / a.k_blocks;
     const int cb = rest % a.c_blocks;
@@ -671,6 +657,27 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
             }
         }
     }
+}
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
+__global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
+    direct_dw_block<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>(a, blockIdx.x, gridDim.x);
+}
+
+// Both backward passes in one launch: blocks [0, nbx) compute dX (the
+// forward kernel on G with the transposed, flipped filter), the rest the dW
+// partials.  The dX blocks are dispatched first, so dW blocks fill the CUs
+// as dX blocks retire instead of waiting for a kernel boundary.  Dynamic LDS
+// is the larger of the two needs.
+template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XCC, bool XWVEC, int KT, int CT,
+          int ROWS, int CC, int GPC, int WKF, bool FULL>
+__global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
+                                                            const DirectDwArgs dw, int nbx) {
+    if ((int)blockIdx.x < nbx)
+        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XCC, 1, XWVEC>(dx, blockIdx.x, nbx);
+    else
+        direct_dw_block<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>(dw, blockIdx.x - nbx,
+                                                                gridDim.x - nbx);
 }
 
 // dw[e] = beta*dw[e] + sum_s part[s][e].  Thread (e4, grp) sums splits

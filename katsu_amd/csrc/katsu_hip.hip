@@ -46,7 +46,7 @@ struct State {
     bool ready = false;
     int device = -1;
     hipStream_t stream = nullptr;
-    Buffer staging[4];
+    Buffer staging[5];
     Buffer workspace;
 };
 
@@ -291,8 +291,16 @@ struct DirectFwdProblem {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// A planned direct forward-shaped launch: arguments, grid, weight path.
+struct DirectFwdPlan {
+    bool ok = false;
+    DirectArgs a;
+    int64_t blocks = 0;
+    bool wvec = false;
+};
+
 template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
-bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
     if (P.R != R || P.S != S) return false;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
@@ -319,7 +327,7 @@ bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
         if (rows_max > ROWS) continue;
         const int64_t blocks = co_blocks * P.N * ntiles;
         if (blocks < kMinDirectBlocks || blocks > kI32Max) return false;
-        DirectArgs a;
+        DirectArgs &a = pl->a;
         a.in = P.in;
         a.w = P.w;
         a.out = P.out;
@@ -345,29 +353,56 @@ bool direct_fwd_launch(const DirectFwdProblem &P, hipStream_t st, int *rc) {
         a.out_vec = (tile_px % 4 == 0 && OHW % 4 == 0 && aligned16(P.out)) ? 1 : 0;
         a.beta = P.beta;
         a.fd_ow = fdiv(P.OW);
-        // 16-byte weight rows: every row start must be 16-byte aligned.
-        const bool wvec = (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w) &&
-                          (CB * R * S) % 4 == 0 && (KT * R * S) % 4 == 0;
-        if (wvec) {
-            constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, true>;
-            if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
-            kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
-        } else {
-            constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, false>;
-            if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
-            kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(a);
-        }
-        *rc = launch_status();
+        // 16-byte weight loads: every float4 of a chunk row must lie inside
+        // the row, which holds when rows start and end on multiples of 4.
+        pl->wvec = (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w);
+        pl->blocks = blocks;
+        pl->ok = true;
         return true;
     }
     return false;
 }
 
-// Forward variants in order of preference; false = none applies.
+template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
+    int rc;
+    if (pl.wvec) {
+        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, true>;
+        if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
+        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
+    } else {
+        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, false>;
+        if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
+        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
+    }
+    return launch_status();
+}
+
+// The direct forward variant: 64 output channels x 13 fragments per block,
+// 8-channel chunks, 3x3 filters, 7 halo rows of 64 columns.
+struct FwdV {
+    static constexpr int KT = 64, F = 13, CB = 8, R = 3, S = 3, ROWS = 7, CC = 1;
+};
+#define KATSU_FWD_VARIANT FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::CC
+
+// Forward-shaped direct launch; false = the variant does not apply.
 template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
-    if (P.CO >= 64 && direct_fwd_launch<64, 13, 8, 3, 3, 7, 1, WMODE>(P, st, rc)) return true;
-    return false;
+    DirectFwdPlan pl;
+    if (P.CO < 64 || !direct_fwd_plan<KATSU_FWD_VARIANT, WMODE>(P, &pl)) return false;
+    *rc = direct_fwd_run<KATSU_FWD_VARIANT, WMODE>(pl, st);
+    return true;
+}
+
+// The data gradient as a forward problem (stride 1 only): G convolved with
+// the transposed, flipped filter, padding R-1-pad (rows) / S-1-pad (columns).
+bool dx_as_forward(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+                   DirectFwdProblem *P) {
+    if (d.st != 1 || d.pad > d.R - 1 || d.pad > d.S - 1) return false;
+    *P = DirectFwdProblem{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1,
+                          d.R - 1 - d.pad, d.S - 1 - d.pad, d.H, d.W, beta};
+    return true;
 }
 
 // Filter gradient.  Plan first (the workspace size is part of the API), then launch.
@@ -518,17 +553,22 @@ int dw_kernel_launch(const DirectDwPlan &pl, hipStream_t st) {
     return launch_status();
 }
 
-int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw, float beta,
-                     float *ws, hipStream_t st) {
-    DirectDwArgs &a = pl.a;
-    const bool direct = pl.splits == 1;
+// Binds the operands of a planned direct dW launch.
+void dw_bind(DirectDwPlan *pl, const float *x, const float *gy, float *dw, float beta, float *ws) {
+    DirectDwArgs &a = pl->a;
+    const bool direct = pl->splits == 1;
     a.x = x;
     a.g = gy;
     a.out = direct ? dw : ws;
-    a.split_stride = direct ? 0 : pl.pstride;
+    a.split_stride = direct ? 0 : pl->pstride;
     a.beta = direct ? beta : 0.f;
     if (!aligned16(gy)) a.g_vec = 0;
     if (!aligned16(a.out)) a.out_vec = 0;
+}
+
+int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw, float beta,
+                     float *ws, hipStream_t st) {
+    dw_bind(&pl, x, gy, dw, beta, ws);
     int rc = KATSU_E_INVALID;
     switch (pl.variant) {
 #define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)                      \
@@ -540,8 +580,62 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
 #undef KATSU_DW_CASE
         default: return KATSU_E_INVALID;
     }
-    if (rc != KATSU_OK || direct) return rc;
-    return launch_split_reduce(ws, dw, (int64_t)a.K * a.CRS, pl.pstride, pl.splits, beta, st);
+    if (rc != KATSU_OK || pl.splits == 1) return rc;
+    return launch_split_reduce(ws, dw, (int64_t)pl.a.K * pl.a.CRS, pl.pstride, pl.splits, beta,
+                               st);
+}
+
+// dX and dW in one launch (direct_bwd_kernel): the direct dX plan and a
+// direct dW variant with the same filter size.
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL,
+          bool XWVEC>
+int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
+    using XGeo = DirectFwdGeo<KATSU_FWD_VARIANT, 1>;
+    constexpr auto kern = direct_bwd_kernel<FwdV::KT, FwdV::F, FwdV::CB, R, S, FwdV::ROWS,
+                                            FwdV::CC, XWVEC, KT, CT, ROWS, CC, GPC, WKF, FULL>;
+    const int rc = lds_optin<kern>(kLdsMax);
+    if (rc != KATSU_OK) return rc;
+    const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
+    kern<<<dim3((unsigned)(xp.blocks + wp.blocks)), dim3(256), lds, st>>>(xp.a, wp.a,
+                                                                         (int)xp.blocks);
+    return launch_status();
+}
+
+template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF>
+int bwd_fused_variant(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
+    if constexpr (R == FwdV::R && S == FwdV::S) {
+        if (wp.full)
+            return xp.wvec ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true, true>(xp, wp, st)
+                           : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true, false>(xp, wp, st);
+        return xp.wvec ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false, true>(xp, wp, st)
+                       : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false, false>(xp, wp, st);
+    }
+    return KATSU_E_INVALID;
+}
+
+// Whether a dW variant can share a launch with the direct dX kernel.
+bool dw_variant_fusable(int variant) {
+#define KATSU_DW_FUSABLE(id, kt, ct, r, s, rows, cc, gpc, wkf, tb) \
+    if (variant == id) return r == FwdV::R && s == FwdV::S;
+    KATSU_DW_VARIANTS(KATSU_DW_FUSABLE)
+#undef KATSU_DW_FUSABLE
+    return false;
+}
+
+int bwd_fused_launch(const DirectFwdPlan &xp, DirectDwPlan wp, const float *x, const float *gy,
+                     float *dw, float beta, float *ws, hipStream_t st) {
+    dw_bind(&wp, x, gy, dw, beta, ws);
+    int rc = KATSU_E_INVALID;
+    switch (wp.variant) {
+#define KATSU_DW_FUSED(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)              \
+    case id: rc = bwd_fused_variant<KT, CT, R, S, ROWS, CC, GPC, WKF>(xp, wp, st); break;
+        KATSU_DW_VARIANTS(KATSU_DW_FUSED)
+#undef KATSU_DW_FUSED
+        default: return KATSU_E_INVALID;
+    }
+    if (rc != KATSU_OK || wp.splits == 1) return rc;
+    return launch_split_reduce(ws, dw, (int64_t)wp.a.K * wp.a.CRS, wp.pstride, wp.splits, beta,
+                               st);
 }
 
 // ---------------------------------------------------------------------------
@@ -671,11 +765,8 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
     if (d.npix_in == 0) return KATSU_OK;
     if (!gy || !w || !dx) return KATSU_E_INVALID;
-    // Stride 1: dX is a forward convolution of G with the transposed, flipped
-    // filter and padding R-1-pad (rows) / S-1-pad (columns).
-    if (d.st == 1 && d.pad <= d.R - 1 && d.pad <= d.S - 1) {
-        DirectFwdProblem P{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1,
-                           d.R - 1 - d.pad, d.S - 1 - d.pad, d.H, d.W, beta};
+    DirectFwdProblem P;
+    if (dx_as_forward(d, gy, w, dx, beta, &P)) {
         int rc = KATSU_OK;
         if (direct_fwd<1>(P, st, &rc)) return rc;
     }
@@ -795,6 +886,41 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     }
     if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
+}
+
+// Both backward passes (backward_buffers, conv2d.rs:265-292).  When dX and
+// dW both take their direct kernels they run as one launch; otherwise dX then
+// dW, as two.
+int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, float *dw,
+                 const katsu_conv_geom *g, float beta, void *ws, size_t ws_bytes, hipStream_t st,
+                 Buffer *fallback) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    if (!dx || !dw) return KATSU_E_INVALID;
+    DirectFwdProblem P;
+    DirectFwdPlan xp;
+    DwPlan wpl;
+    const bool fused = d.npix_out > 0 && x && w && gy && dx_as_forward(d, gy, w, dx, beta, &P) &&
+                       P.CO >= FwdV::KT && direct_fwd_plan<KATSU_FWD_VARIANT, 1>(P, &xp) &&
+                       (wpl = dw_plan_any(d)).direct.ok && dw_variant_fusable(wpl.direct.variant);
+    if (!fused) {
+        const int rc = conv_bwd_data_dev(gy, w, dx, g, beta, st);
+        if (rc != KATSU_OK) return rc;
+        return conv_bwd_filter_dev(x, gy, dw, g, beta, ws, ws_bytes, st, fallback);
+    }
+    float *wsp = (float *)ws;
+    if (wpl.ws_bytes > 0) {
+        if (!wsp) {
+            if (!fallback) return KATSU_E_INVALID;
+            const int rc = ensure(*fallback, wpl.ws_bytes);
+            if (rc != KATSU_OK) return rc;
+            wsp = (float *)fallback->ptr;
+        } else if (ws_bytes < wpl.ws_bytes) {
+            return KATSU_E_INVALID;
+        }
+    }
+    return bwd_fused_launch(xp, wpl.direct, x, gy, dw, beta, wsp, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -979,6 +1105,55 @@ int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *
     std::lock_guard<std::mutex> lock(s.mu);
     return conv_bwd_filter_dev(x, gy, dw, g, beta, nullptr, 0, (hipStream_t)stream,
                                &s.workspace);
+}
+
+int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy, float *dx,
+                                 float *dw, const katsu_conv_geom *g, float beta, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+    if (workspace) {
+        return conv_bwd_dev(x, w, gy, dx, dw, g, beta, workspace, workspace_bytes,
+                            (hipStream_t)stream, nullptr);
+    }
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return conv_bwd_dev(x, w, gy, dx, dw, g, beta, nullptr, 0, (hipStream_t)stream,
+                        &s.workspace);
+}
+
+int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
+                             float *dw, const katsu_conv_geom *g, float beta) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    const size_t nx = (size_t)d.npix_in * d.C, nw = (size_t)d.K * d.CRS,
+                 ny = (size_t)d.npix_out * d.K;
+    if (!dw || (nx > 0 && !dx)) return KATSU_E_INVALID;
+    if (ny > 0 && (!x || !w || !gy)) return KATSU_E_INVALID;
+    if (ny == 0) return host_scale(dw, nw, beta);  // empty batch: dx is empty, dw = beta*dw
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    if ((rc = h2d(s.staging[0], x, nx, s.stream))) return rc;
+    if ((rc = h2d(s.staging[1], w, nw, s.stream))) return rc;
+    if ((rc = h2d(s.staging[2], gy, ny, s.stream))) return rc;
+    if (beta != 0.f) {
+        if ((rc = h2d(s.staging[3], dx, nx, s.stream))) return rc;
+        if ((rc = h2d(s.staging[4], dw, nw, s.stream))) return rc;
+    } else {
+        if ((rc = ensure(s.staging[3], nx * sizeof(float)))) return rc;
+        if ((rc = ensure(s.staging[4], nw * sizeof(float)))) return rc;
+    }
+    rc = conv_bwd_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
+                      (const float *)s.staging[2].ptr, (float *)s.staging[3].ptr,
+                      (float *)s.staging[4].ptr, g, beta, nullptr, 0, s.stream, &s.workspace);
+    if (rc) return rc;
+    if (nx > 0) {
+        rc = map_hip(hipMemcpyAsync(dx, s.staging[3].ptr, nx * sizeof(float),
+                                    hipMemcpyDeviceToHost, s.stream));
+        if (rc) return rc;
+    }
+    return d2h_sync(dw, s.staging[4], nw, s.stream);
 }
 
 int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,

@@ -37,10 +37,8 @@ def conv2d_backward(x, w, gy, stride, pad):
         raise ValueError("grad length must match the output")
     dx = np.zeros(x.shape, np.float32)
     dw = np.zeros(w.shape, np.float32)
-    check(lib().katsu_hip_conv2d_bwd_data_f32(_p(gy), _p(w), _p(dx), ctypes.byref(g), 0.0),
-          "conv2d_bwd_data")
-    check(lib().katsu_hip_conv2d_bwd_filter_f32(_p(x), _p(gy), _p(dw), ctypes.byref(g), 0.0),
-          "conv2d_bwd_filter")
+    check(lib().katsu_hip_conv2d_bwd_f32(_p(x), _p(w), _p(gy), _p(dx), _p(dw), ctypes.byref(g),
+                                         0.0), "conv2d_bwd")
     return dx, dw
 
 

@@ -83,6 +83,25 @@ def conv2d_backward_filter(x, gy, wshape, stride, pad, out=None, beta=0.0, works
     return out
 
 
+def conv2d_backward(x, w, gy, stride, pad, dx=None, dw=None, beta=0.0, workspace=None):
+    """(dx, dw) of backward_buffers (conv2d.rs:265-292) in one call; beta=1
+    accumulates into `dx` and `dw`.  When both passes take the direct gfx950
+    kernels they run as a single launch.  `workspace` as for
+    conv2d_backward_filter."""
+    _dev_f32(x, w, gy, dx, dw)
+    g = conv_geom(x.shape, w.shape, stride, pad)
+    if dx is None:
+        dx = torch.empty(tuple(x.shape), device=x.device, dtype=torch.float32)
+    if dw is None:
+        dw = torch.empty(tuple(w.shape), device=x.device, dtype=torch.float32)
+    ws = ctypes.c_void_p(workspace.data_ptr()) if workspace is not None else ctypes.c_void_p(0)
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib().katsu_hip_conv2d_bwd_f32_dev(_p(x), _p(w), _p(gy), _p(dx), _p(dw),
+                                              ctypes.byref(g), float(beta), ws, wsb, _stream()),
+          "conv2d_bwd")
+    return dx, dw
+
+
 def gemm(a, b, m, n, k, trans_a=False, trans_b=False, out=None, beta=0.0):
     """out[m,n] = beta*out + op(a) op(b) (tensor.rs:264-273, 424-444)."""
     _dev_f32(a, b, out)
