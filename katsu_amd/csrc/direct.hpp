@@ -89,38 +89,53 @@ __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0
 // the KT channels into 16-row slices and the pixel range into WPX parts of
 // F fragments of 16 pixels each.  Input channels are consumed CB at a time
 // through a two-stage LDS pipeline.
+//
+// Three weight modes (WMODE) make the same kernel serve three problems:
+//   0  forward:  w' = w[CO][CI][R][S] as stored
+//   1  dX, stride 1: in = G, w'[co][ci][r][s] = w[ci][co][R-1-r][S-1-s]
+//   2  dX, stride 2, by super-pixels: in = G, output channel co' = 4c + 2py + px
+//      is input pixel (2Y+py, 2X+px) of channel c at super-pixel (Y, X), and
+//      w'[co'][k][a][b] = w[k][c][r][s] with r = py + pad - 2(amin + a),
+//      s = px + pad - 2(bmin + b), zero where (r, s) falls outside the filter.
+//      The conv over super-pixels is stride 1 with filter R' x S' and
+//      padding (-amin, -bmin); the epilogue (EPI 1) scatters co' back to
+//      channel c, pixel (2Y+py, 2X+px).
 struct DirectArgs {
     const float *in;   // [N][CI][H][W]
-    const float *w;    // layer weights: WMODE 0 w[CO][CI][R][S]; WMODE 1 w[CI][CO][R][S]
-    float *out;        // [N][CO][OH][OW]
+    const float *w;    // layer weights (see WMODE)
+    float *out;        // [N][CO][OH][OW]; EPI 1: [N][CO/4][fh][fw]
     int N, CI, H, W, CO, OH, OW, st, pady, padx;
     int OHW, HW;
-    int64_t in_img, out_img;  // CI*H*W, CO*OH*OW
+    int64_t in_img, out_img;  // CI*H*W, output floats per image
     int tile_px;       // output pixels per tile (one image)
     int tiles_img;     // tiles per image
     int co_blocks;     // ceil(CO / KT)
-    int ncols;         // halo columns: (OW-1)*st + S  (<= 64*CC)
+    int ncols;         // halo columns: (OW-1)*st + S  (<= PITCH)
     uint32_t w_bytes;  // size of w
     int out_vec;       // 1: tile_px and OHW are multiples of 4 (16-byte output runs)
     float beta;        // out = beta*out + result (beta in {0, 1})
     FastDiv fd_ow;     // division by OW
+    // WMODE 2 / EPI 1: the layer's C, R, S, padding, the super-filter's
+    // offsets, C*R*S, and the full-resolution output size.
+    int g_c, g_r, g_s, g_pad, g_amin, g_bmin, g_crs, fh, fw;
 };
 
 // LDS layout (floats) of the forward kernel.
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE>
 struct DirectFwdGeo {
     static constexpr int RS = R * S;
-    static constexpr int PITCH = 64 * CC;               // halo row pitch
+    static_assert(PITCH == 32 || PITCH % 64 == 0, "halo row pitch: 32 or a multiple of 64");
+    static_assert(PITCH != 32 || ROWS % 2 == 0, "32-float rows are staged in pairs");
     static constexpr int CPITCH = ROWS * PITCH + 16;    // channel pitch, == 16 (mod 32)
     static constexpr int XS = CB * CPITCH;              // input tile
     // Weight tile, kept in the global order of its rows:
-    //   WMODE 0: KT rows (co) of CB*RS floats, pitch CB*RS + 4
-    //   WMODE 1: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
+    //   WMODE 0, 2: KT rows (co) of CB*RS floats, pitch CB*RS + 4
+    //   WMODE 1:    CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
     // Pitches are multiples of 4 floats so 16-byte DMA lands on row
     // boundaries; the region is a whole number of 256-float wave loads.
-    static constexpr int WROWS = WMODE == 0 ? KT : CB;
-    static constexpr int WLEN = WMODE == 0 ? CB * RS : KT * RS;
-    static constexpr int WPITCH = WMODE == 0 ? WLEN + 4 : WLEN + ((16 - WLEN % 32) + 32) % 32;
+    static constexpr int WROWS = WMODE == 1 ? CB : KT;
+    static constexpr int WLEN = WMODE == 1 ? KT * RS : CB * RS;
+    static constexpr int WPITCH = WMODE == 1 ? WLEN + ((16 - WLEN % 32) + 32) % 32 : WLEN + 4;
     static constexpr int WS = (WROWS * WPITCH + 255) / 256 * 256;
     static_assert(WLEN % 4 == 0 && WPITCH % 4 == 0, "weight rows of whole float4");
     static constexpr int STAGE = XS + WS;
@@ -129,18 +144,24 @@ struct DirectFwdGeo {
     static constexpr int YPITCH = TPMAX + 4;
     static_assert(KT * YPITCH <= 2 * STAGE, "output tile must fit the LDS stages");
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+    // WMODE 2 weight slots per lane (4-byte wave loads spread over 4 waves).
+    static constexpr int WSLOTS = (WS / 64 + 3) / 4;
 };
 
 // Block `bid` of `nb` (the kernel below, or the dX half of the fused
 // backward launch).
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE, bool WVEC>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
+          bool WVEC>
 __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     constexpr int RS = R * S;
     constexpr int WOC = KT / 16;            // waves along output channels
     constexpr int CPW = CB / 4;             // input channels staged per wave
+    constexpr int RPL = PITCH >= 64 ? 1 : 64 / PITCH;   // halo rows per wave load
+    constexpr int LPR = PITCH >= 64 ? PITCH / 64 : 1;   // wave loads per halo row
     static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
     static_assert(CB % 4 == 0, "CB must be a multiple of 4");
+    static_assert(WMODE != 2 || !WVEC, "gathered weights load 4 bytes per lane");
 
     extern __shared__ float smem[];
 
@@ -165,47 +186,79 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         p = p < p1 ? p : p0;
         const int oy = a.fd_ow.div(p);
         const int ox = p - oy * a.OW;
-        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * Geo::PITCH + ox * a.st;
+        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * PITCH + ox * a.st;
     }
     // Per-lane A-fragment base: row co = woc*16 + l%16, channel l/16.
-    const int abase = WMODE == 0
-        ? (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS
-        : (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS;
+    const int abase = WMODE == 1
+        ? (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS
+        : (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS;
 
     // ---- staging: LDS-direct loads ------------------------------------------
-    // Input halo: wave w stages channels w + 4j (j < CPW), one 64-column
-    // row chunk per load.  Weights: 16-byte loads when every float4 of a row
-    // lies inside the row (WVEC), else 4-byte loads.  Padding, rows past the
-    // image and channels past the count read as zeros.
+    // Input halo: wave w stages channels w + 4j (j < CPW), one 64-float run
+    // per load (a row chunk, or two 32-float rows).  Weights: 16-byte loads
+    // when every float4 of a row lies inside the row (WVEC), else 4-byte
+    // loads (WMODE 2: gathered through a per-lane table).  Padding, rows past
+    // the image and channels past the count read as zeros.
     const __amdgpu_buffer_rsrc_t rin =
         buf_rsrc(a.in + (int64_t)n * a.in_img, (uint32_t)(a.in_img * 4));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, a.w_bytes);
-    int colb[CC];  // byte offset of the lane's column within a row, or kOOB
+    const int lrow = PITCH >= 64 ? 0 : lane / PITCH;  // the lane's row within a load
+    int colb[LPR];  // byte offset of the lane's column within a row, or kOOB
 #pragma unroll
-    for (int c = 0; c < CC; ++c) {
-        const int col = c * 64 + lane;
+    for (int c = 0; c < LPR; ++c) {
+        const int col = c * 64 + (PITCH >= 64 ? lane : lane % PITCH);
         const int ix = col - a.padx;
         colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
     const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform wave index
+
+    // WMODE 2: per lane and weight slot, the float offset of the element for
+    // input channel 0 (the chunk adds ci0 * C*R*S), or -1 for a zero.
+    int wtab[WMODE == 2 ? Geo::WSLOTS : 1];
+    if (WMODE == 2) {
+#pragma unroll
+        for (int q = 0; q < Geo::WSLOTS; ++q) {
+            const int e = (q * 4 + wv) * 64 + lane;
+            const int row = e / Geo::WPITCH, col = e - (e / Geo::WPITCH) * Geo::WPITCH;
+            const int ci = col / RS, tap = col - (col / RS) * RS;
+            const int co = co0 + row;
+            const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
+            const int r = py + a.g_pad - 2 * (a.g_amin + tap / S);
+            const int sx = px + a.g_pad - 2 * (a.g_bmin + tap % S);
+            const bool ok = row < KT && col < Geo::WLEN && co < a.CO &&
+                            (unsigned)r < (unsigned)a.g_r && (unsigned)sx < (unsigned)a.g_s;
+            wtab[q] = ok ? ci * a.g_crs + (c * a.g_r + r) * a.g_s + sx : -1;
+        }
+    }
 
     auto stage_in = [&](float *stage, int ci0) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
             const int ci = ci0 + wv + 4 * j;
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const int iy = iy0 + r;
+            for (int r = 0; r < ROWS; r += RPL) {
+                const int iy = iy0 + r + lrow;
                 const bool rok = ci < a.CI && (unsigned)iy < (unsigned)a.H;
                 const int rowb = (ci * a.H + iy) * a.W * 4;
 #pragma unroll
-                for (int c = 0; c < CC; ++c)
-                    lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * Geo::PITCH + c * 64,
+                for (int c = 0; c < LPR; ++c)
+                    lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
                                 rok ? rowb + colb[c] : kOOB);
             }
         }
-        // Valid floats of a weight row in this chunk, and its global start.
         float *wst = stage + Geo::XS;
+        if (WMODE == 2) {
+            constexpr int NI = Geo::WS / 64;
+#pragma unroll
+            for (int q = 0; q < Geo::WSLOTS; ++q) {
+                const int i = q * 4 + wv;
+                if (i < NI)
+                    lds_dma_b32(rw, wst + i * 64,
+                                wtab[q] >= 0 ? (wtab[q] + ci0 * a.g_crs) * 4 : kOOB);
+            }
+            return;
+        }
+        // Valid floats of a weight row in this chunk, and its global start.
         auto woff = [&](int row, int col) __attribute__((always_inline)) {
             if (WMODE == 0) {
                 const int co = co0 + row;
@@ -256,8 +309,8 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         const int cs = kk / RS, tap = kk % RS;
         const int r = tap / S, s = tap % S;
         const float *ws = base + Geo::XS + abase;
-        av = WMODE == 0 ? ws[cs * 4 * RS + tap] : ws[cs * 4 * Geo::WPITCH + (RS - 1 - tap)];
-        const int toff = cs * 4 * Geo::CPITCH + r * Geo::PITCH + s;
+        av = WMODE == 1 ? ws[cs * 4 * Geo::WPITCH + (RS - 1 - tap)] : ws[cs * 4 * RS + tap];
+        const int toff = cs * 4 * Geo::CPITCH + r * PITCH + s;
 #pragma unroll
         for (int f = 0; f < F; ++f) b[f] = base[pix[f] + toff];
     };
@@ -308,7 +361,8 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
 
     // Epilogue: transpose the KT x tile block through LDS (the stages are
     // free after the last barrier), then write each output channel's pixel
-    // run -- contiguous in NCHW -- as 16-byte stores.
+    // run -- contiguous in NCHW -- as 16-byte stores (EPI 0), or scatter each
+    // super-pixel channel to its full-resolution positions (EPI 1).
     float *ys = smem;
 #pragma unroll
     for (int f = 0; f < F; ++f)
@@ -319,7 +373,21 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
     const int np = p1 - p0;
-    if (a.out_vec) {
+    if (EPI == 1) {
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
+            float *dst = outb + (int64_t)c * a.fh * a.fw;
+            for (int p = lane; p < np; p += 64) {
+                const int Y = a.fd_ow.div(p0 + p);
+                const int X = p0 + p - Y * a.OW;
+                const int iy = 2 * Y + py, ix = 2 * X + px;
+                if (iy < a.fh && ix < a.fw)
+                    store_beta(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], a.beta);
+            }
+        }
+    } else if (a.out_vec) {
         const int n4 = np >> 2;
         for (int row = wave; row < KT; row += 4) {
             const int co = co0 + row;
@@ -343,9 +411,10 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     }
 }
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE, bool WVEC>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
+          bool WVEC>
 __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
-    direct_fwd_block<KT, F, CB, R, S, ROWS, CC, WMODE, WVEC>(a, blockIdx.x, gridDim.x);
+    direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WVEC>(a, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -669,12 +738,12 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
 // partials.  The dX blocks are dispatched first, so dW blocks fill the CUs
 // as dX blocks retire instead of waiting for a kernel boundary.  Dynamic LDS
 // is the larger of the two needs.
-template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XCC, bool XWVEC, int KT, int CT,
-          int ROWS, int CC, int GPC, int WKF, bool FULL>
+template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XPITCH, bool XWVEC, int KT,
+          int CT, int ROWS, int CC, int GPC, int WKF, bool FULL>
 __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
                                                             const DirectDwArgs dw, int nbx) {
     if ((int)blockIdx.x < nbx)
-        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XCC, 1, XWVEC>(dx, blockIdx.x, nbx);
+        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC>(dx, blockIdx.x, nbx);
     else
         direct_dw_block<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>(dw, blockIdx.x - nbx,
                                                                 gridDim.x - nbx);

@@ -282,11 +282,15 @@ int lds_optin(size_t bytes) {
 }
 
 // A "forward-shaped" problem: out[n][co] = sum_ci,taps in[n][ci] * w'.
+// For the super-pixel data gradient (WMODE 2) the extra fields describe the
+// layer (C, R, S, padding), the super-filter's first offsets and the
+// full-resolution output; they are unused otherwise.
 struct DirectFwdProblem {
     const float *in, *w;
     float *out;
     int64_t N, CI, H, W, CO, R, S, st, pady, padx, OH, OW;
     float beta;
+    int64_t g_c = 0, g_r = 0, g_s = 0, g_pad = 0, g_amin = 0, g_bmin = 0, fh = 0, fw = 0;
 };
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -299,18 +303,18 @@ struct DirectFwdPlan {
     bool wvec = false;
 };
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE>
 bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     if (P.R != R || P.S != S) return false;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
     constexpr int WPX = 4 / (KT / 16);
     const int64_t OHW = P.OH * P.OW;
     const int64_t ncols = (P.OW - 1) * P.st + S;
-    if (ncols > 64 * CC) return false;
+    if (ncols > PITCH) return false;
     // Buffer resources address one image of `in` and all of `w` in bytes.
     const int64_t in_img = P.CI * P.H * P.W;
-    const int64_t w_elems = P.CO * P.CI * R * S;
+    const int64_t w_elems = WMODE == 2 ? P.CI * P.g_c * P.g_r * P.g_s : P.CO * P.CI * R * S;
     if (in_img * 4 >= (int64_t)kMaxBufBytes || w_elems * 4 >= (int64_t)kMaxBufBytes) return false;
     const int64_t co_blocks = cdiv(P.CO, KT);
     const int64_t tpmax = (int64_t)WPX * F * 16;
@@ -318,13 +322,16 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     // lengths rounded to whole 16-byte output runs when that still fits.
     int64_t tiles_img = std::max(cdiv(OHW, tpmax), cdiv(kMinDirectBlocks, co_blocks * P.N));
     for (int attempt = 0; attempt < 64; ++attempt, ++tiles_img) {
-        int64_t tile_px = cdiv(OHW, tiles_img);
-        if (tile_px % 4 != 0 && (tile_px + 3) / 4 * 4 <= tpmax) tile_px = (tile_px + 3) / 4 * 4;
-        if (tile_px > tpmax) continue;
-        if (2 * tile_px < tpmax) return false;  // fragments would be under half full
+        const int64_t even = cdiv(OHW, tiles_img);
+        if (even > tpmax) continue;
+        if (2 * even < tpmax) return false;  // fragments would be under half full
+        // A length rounded to whole 16-byte runs first, else the even split
+        // (which can be whole rows where the rounded one is not).
+        auto rows_of = [&](int64_t px) { return (tile_row_span(px, P.OW, P.OH) - 1) * P.st + R; };
+        int64_t tile_px = (even + 3) / 4 * 4;
+        if (tile_px > tpmax || rows_of(tile_px) > ROWS) tile_px = even;
+        if (rows_of(tile_px) > ROWS) continue;
         const int64_t ntiles = cdiv(OHW, tile_px);
-        const int64_t rows_max = (tile_row_span(tile_px, P.OW, P.OH) - 1) * P.st + R;
-        if (rows_max > ROWS) continue;
         const int64_t blocks = co_blocks * P.N * ntiles;
         if (blocks < kMinDirectBlocks || blocks > kI32Max) return false;
         DirectArgs &a = pl->a;
@@ -344,7 +351,7 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
         a.OHW = (int)OHW;
         a.HW = (int)(P.H * P.W);
         a.in_img = in_img;
-        a.out_img = P.CO * OHW;
+        a.out_img = WMODE == 2 ? P.g_c * P.fh * P.fw : P.CO * OHW;
         a.tile_px = (int)tile_px;
         a.tiles_img = (int)ntiles;
         a.co_blocks = (int)co_blocks;
@@ -353,9 +360,18 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
         a.out_vec = (tile_px % 4 == 0 && OHW % 4 == 0 && aligned16(P.out)) ? 1 : 0;
         a.beta = P.beta;
         a.fd_ow = fdiv(P.OW);
+        a.g_c = (int)P.g_c;
+        a.g_r = (int)P.g_r;
+        a.g_s = (int)P.g_s;
+        a.g_pad = (int)P.g_pad;
+        a.g_amin = (int)P.g_amin;
+        a.g_bmin = (int)P.g_bmin;
+        a.g_crs = (int)(P.g_c * P.g_r * P.g_s);
+        a.fh = (int)P.fh;
+        a.fw = (int)P.fw;
         // 16-byte weight loads: every float4 of a chunk row must lie inside
         // the row, which holds when rows start and end on multiples of 4.
-        pl->wvec = (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w);
+        pl->wvec = WMODE != 2 && (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w);
         pl->blocks = blocks;
         pl->ok = true;
         return true;
@@ -363,36 +379,91 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     return false;
 }
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int CC, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI>
 int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, CC, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     int rc;
     if (pl.wvec) {
-        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, true>;
+        constexpr auto kern =
+            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WMODE != 2>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
     } else {
-        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, CC, WMODE, false>;
+        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, false>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
     }
     return launch_status();
 }
 
-// The direct forward variant: 64 output channels x 13 fragments per block,
-// 8-channel chunks, 3x3 filters, 7 halo rows of 64 columns.
-struct FwdV {
-    static constexpr int KT = 64, F = 13, CB = 8, R = 3, S = 3, ROWS = 7, CC = 1;
+// Direct forward-shaped variants: block tile (KT output channels x F
+// fragments per wave), input-channel chunk, filter, halo rows and pitch.
+template <int KT_, int F_, int CB_, int R_, int S_, int ROWS_, int PITCH_>
+struct FwdVariant {
+    static constexpr int KT = KT_, F = F_, CB = CB_, R = R_, S = S_, ROWS = ROWS_, PITCH = PITCH_;
 };
-#define KATSU_FWD_VARIANT FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::CC
+// 3x3 stride 1 (forward and data gradient): 64 x 208-pixel tiles.
+using FwdV = FwdVariant<64, 13, 8, 3, 3, 7, 64>;
+// 3x3 stride 2 forward: 64 x 64-pixel tiles, 32-float halo rows.
+using FwdS2 = FwdVariant<64, 4, 8, 3, 3, 12, 32>;
+// Stride-2 data gradient by super-pixels: a 4x4 super-filter (7x7 layers
+// such as the stem) with few channels, and a 2x2 one (3x3 layers).
+using DxSp4 = FwdVariant<16, 13, 4, 4, 4, 11, 128>;
+using DxSp2 = FwdVariant<64, 7, 16, 2, 2, 8, 32>;
 
-// Forward-shaped direct launch; false = the variant does not apply.
+#define KATSU_FWD_VARIANT FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::PITCH
+
+template <class V, int WMODE, int EPI>
+bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    DirectFwdPlan pl;
+    if (P.CO < V::KT / 2 ||
+        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE>(P, &pl))
+        return false;
+    *rc = direct_fwd_run<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, EPI>(pl, st);
+    return true;
+}
+
+// Forward-shaped direct launch; false = no variant applies.
 template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
-    DirectFwdPlan pl;
-    if (P.CO < 64 || !direct_fwd_plan<KATSU_FWD_VARIANT, WMODE>(P, &pl)) return false;
-    *rc = direct_fwd_run<KATSU_FWD_VARIANT, WMODE>(pl, st);
-    return true;
+    if (P.st == 1 && P.CO >= FwdV::KT) return try_direct<FwdV, WMODE, 0>(P, st, rc);
+    if (WMODE == 0 && P.st == 2) return try_direct<FwdS2, 0, 0>(P, st, rc);
+    return false;
+}
+
+// The stride-2 data gradient as a stride-1 problem over super-pixels (see
+// direct.hpp, WMODE 2): input G, 4C output channels, super-filter offsets
+// [amin, amax] per axis.
+bool dx_superpixel(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+                   hipStream_t st, int *rc) {
+    if (d.st != 2) return false;
+    auto range = [&](int64_t R, int64_t *lo, int64_t *hi) {
+        *lo = INT64_MAX;
+        *hi = INT64_MIN;
+        for (int64_t p = 0; p < 2; ++p)
+            for (int64_t r = 0; r < R; ++r) {
+                const int64_t e = p + d.pad - r;
+                if (e % 2 != 0) continue;
+                *lo = std::min(*lo, e / 2);
+                *hi = std::max(*hi, e / 2);
+            }
+    };
+    int64_t amin, amax, bmin, bmax;
+    range(d.R, &amin, &amax);
+    range(d.S, &bmin, &bmax);
+    DirectFwdProblem P{gy, w, dx, d.N, d.K, d.OH, d.OW, 4 * d.C, amax - amin + 1,
+                       bmax - bmin + 1, 1, -amin, -bmin, (d.H + 1) / 2, (d.W + 1) / 2, beta};
+    P.g_c = d.C;
+    P.g_r = d.R;
+    P.g_s = d.S;
+    P.g_pad = d.pad;
+    P.g_amin = amin;
+    P.g_bmin = bmin;
+    P.fh = d.H;
+    P.fw = d.W;
+    if (P.R == DxSp4::R && P.S == DxSp4::S && P.CO <= 16) return try_direct<DxSp4, 2, 1>(P, st, rc);
+    if (P.R == DxSp2::R && P.S == DxSp2::S) return try_direct<DxSp2, 2, 1>(P, st, rc);
+    return false;
 }
 
 // The data gradient as a forward problem (stride 1 only): G convolved with
@@ -592,7 +663,7 @@ template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool
 int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
     using XGeo = DirectFwdGeo<KATSU_FWD_VARIANT, 1>;
     constexpr auto kern = direct_bwd_kernel<FwdV::KT, FwdV::F, FwdV::CB, R, S, FwdV::ROWS,
-                                            FwdV::CC, XWVEC, KT, CT, ROWS, CC, GPC, WKF, FULL>;
+                                            FwdV::PITCH, XWVEC, KT, CT, ROWS, CC, GPC, WKF, FULL>;
     const int rc = lds_optin<kern>(kLdsMax);
     if (rc != KATSU_OK) return rc;
     const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
@@ -766,10 +837,9 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     if (d.npix_in == 0) return KATSU_OK;
     if (!gy || !w || !dx) return KATSU_E_INVALID;
     DirectFwdProblem P;
-    if (dx_as_forward(d, gy, w, dx, beta, &P)) {
-        int rc = KATSU_OK;
-        if (direct_fwd<1>(P, st, &rc)) return rc;
-    }
+    int rc = KATSU_OK;
+    if (dx_as_forward(d, gy, w, dx, beta, &P) && direct_fwd<1>(P, st, &rc)) return rc;
+    if (dx_superpixel(d, gy, w, dx, beta, st, &rc)) return rc;
     if (d.C <= 16) return dx_cfg<CfgS>(gy, w, dx, d, beta, st);
     if (d.C <= 64) return dx_cfg<CfgM>(gy, w, dx, d, beta, st);
     return dx_cfg<CfgL>(gy, w, dx, d, beta, st);
