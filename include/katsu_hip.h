@@ -131,6 +131,53 @@ int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy
                                  float *dw, const katsu_conv_geom *g, float beta,
                                  void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- Device residency and the engine's elementwise work -----------------
+ * For callers that keep tensor data on the GPU between calls (a device
+ * mirror per immutable node, tensor.rs:96-107), accumulate adjoints in
+ * device pending buffers (tensor.rs:327-360) and run the elementwise ops,
+ * sum and their VJPs there (tensor.rs:217-247, 392-417).  No reference
+ * function corresponds to the buffer calls: the reference has no device.
+ *
+ * katsu_hip_stream: the library's stream (initialising the library).
+ * katsu_hip_malloc/free: device memory from a caching pool; a freed block is
+ * reused by later allocations in stream order, so callers that use other
+ * streams synchronise before freeing.  All blocks are released by
+ * katsu_hip_shutdown.
+ * katsu_hip_upload/download: count floats host->device / device->host;
+ * both return after the copy completes. */
+void *katsu_hip_stream(void);
+int katsu_hip_malloc(void **ptr, size_t bytes);
+int katsu_hip_free(void *ptr);
+int katsu_hip_upload(void *dst, const float *src, size_t count, void *stream);
+int katsu_hip_download(float *dst, const void *src, size_t count, void *stream);
+int katsu_hip_sync(void *stream);
+
+/* c = beta*c + (a + b) and c = beta*c + a*b over n floats, beta in {0, 1}:
+ * Tensor::add / Tensor::mul (tensor.rs:217-240) with beta 0; Mul's VJP
+ * pending[a] += g*b (tensor.rs:398-409) with beta 1.  Bit-identical to the
+ * reference's loops. */
+int katsu_hip_add_f32_dev(const float *a, const float *b, float *c, size_t n, float beta,
+                          void *stream);
+int katsu_hip_mul_f32_dev(const float *a, const float *b, float *c, size_t n, float beta,
+                          void *stream);
+/* y += x (Add's VJP, tensor.rs:392-397; publishing pending into an existing
+ * gradient, tensor.rs:349-357).  Bit-identical. */
+int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, void *stream);
+/* x = value (fresh zero buffers, tensor.rs:120-125 and 328-331). */
+int katsu_hip_fill_f32_dev(float *x, size_t n, float value, void *stream);
+/* y += s[0] with s on the device (Sum's VJP, tensor.rs:410-417). */
+int katsu_hip_add_scalar_f32_dev(const float *s, float *y, size_t n, void *stream);
+/* out[0] = beta*out[0] + sum(x) (Tensor::sum, tensor.rs:242-247).  A fixed
+ * tree, identical run to run; it differs from the reference's sequential
+ * fold within the f32 summation bound. */
+int katsu_hip_sum_f32_dev(const float *x, size_t n, float *out, float beta, void *stream);
+/* The stem workload's pooling chain (config 5): out[r] = sum_c y[r][c] / cols,
+ * and its VJP dy[r][c] = beta*dy[r][c] + scale*g[r]. */
+int katsu_hip_mean_rows_f32_dev(const float *y, size_t rows, size_t cols, float *out,
+                                void *stream);
+int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, float scale,
+                                     float *dy, float beta, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

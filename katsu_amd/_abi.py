@@ -21,6 +21,11 @@ EXPORTS = (
     "katsu_hip_conv2d_bwd_filter_workspace",
     "katsu_hip_conv2d_bwd_filter_f32", "katsu_hip_conv2d_bwd_filter_f32_dev",
     "katsu_hip_conv2d_bwd_f32", "katsu_hip_conv2d_bwd_f32_dev",
+    "katsu_hip_stream", "katsu_hip_malloc", "katsu_hip_free", "katsu_hip_upload",
+    "katsu_hip_download", "katsu_hip_sync",
+    "katsu_hip_add_f32_dev", "katsu_hip_mul_f32_dev", "katsu_hip_accumulate_f32_dev",
+    "katsu_hip_fill_f32_dev", "katsu_hip_add_scalar_f32_dev", "katsu_hip_sum_f32_dev",
+    "katsu_hip_mean_rows_f32_dev", "katsu_hip_broadcast_rows_f32_dev",
 )
 
 
@@ -68,6 +73,21 @@ def lib():
         L.katsu_hip_conv2d_bwd_filter_f32_dev.argtypes = [vp, vp, vp, gp, fp, vp, sz, vp]
         L.katsu_hip_conv2d_bwd_f32.argtypes = [vp, vp, vp, vp, vp, gp, fp]
         L.katsu_hip_conv2d_bwd_f32_dev.argtypes = [vp, vp, vp, vp, vp, gp, fp, vp, sz, vp]
+        L.katsu_hip_stream.restype = vp
+        L.katsu_hip_stream.argtypes = []
+        L.katsu_hip_malloc.argtypes = [ctypes.POINTER(vp), sz]
+        L.katsu_hip_free.argtypes = [vp]
+        L.katsu_hip_upload.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_download.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_sync.argtypes = [vp]
+        L.katsu_hip_add_f32_dev.argtypes = [vp, vp, vp, sz, fp, vp]
+        L.katsu_hip_mul_f32_dev.argtypes = [vp, vp, vp, sz, fp, vp]
+        L.katsu_hip_accumulate_f32_dev.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_fill_f32_dev.argtypes = [vp, sz, fp, vp]
+        L.katsu_hip_add_scalar_f32_dev.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_sum_f32_dev.argtypes = [vp, sz, vp, fp, vp]
+        L.katsu_hip_mean_rows_f32_dev.argtypes = [vp, sz, sz, vp, vp]
+        L.katsu_hip_broadcast_rows_f32_dev.argtypes = [vp, sz, sz, fp, vp, fp, vp]
         for name in EXPORTS:
             if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown"):
                 getattr(L, name).restype = i

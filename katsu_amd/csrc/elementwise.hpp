@@ -1,0 +1,147 @@
+// elementwise.hpp -- the HBM-bound kernels of the device-resident engine:
+// the elementwise ops and sum of Tensor (tensor.rs:217-247), their VJPs
+// (tensor.rs:392-417), the accumulation of gradients into pending buffers
+// (tensor.rs:327-360) and the mean-pool chain of the stem workload.
+//
+// Every kernel streams its operands once with 16-byte accesses where the
+// pointers and length allow, a grid-stride loop sized to the CU count, and
+// no LDS except in the reductions.  Reductions are deterministic: a fixed
+// assignment of elements to lanes and a fixed combination tree, so a result
+// is identical run to run (it differs from the reference's sequential fold
+// only within the f32 summation bound).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace katsu {
+
+enum class EwOp { Add, Mul };
+
+// c = beta*c + (a OP b), beta in {0, 1}.  With beta = 1 the two roundings are
+// those of `pending[i] += g[i] * other[i]` (tensor.rs:392-409).
+template <EwOp OP, bool VEC>
+__global__ void __launch_bounds__(256) ew_binary(const float *__restrict__ a,
+                                                 const float *__restrict__ b, float *c,
+                                                 int64_t n, float beta) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    auto f = [](float x, float y) { return OP == EwOp::Add ? x + y : x * y; };
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        for (int64_t q = i; q < n4; q += stride) {
+            const float4 x = reinterpret_cast<const float4 *>(a)[q];
+            const float4 y = reinterpret_cast<const float4 *>(b)[q];
+            float4 r = make_float4(f(x.x, y.x), f(x.y, y.y), f(x.z, y.z), f(x.w, y.w));
+            float4 *d = reinterpret_cast<float4 *>(c) + q;
+            if (beta != 0.f) {
+                const float4 o = *d;
+                r = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+            }
+            *d = r;
+        }
+        if (i == 0) {  // the last n % 4 elements
+            for (int64_t e = n4 << 2; e < n; ++e) {
+                const float r = f(a[e], b[e]);
+                c[e] = beta != 0.f ? c[e] + r : r;
+            }
+        }
+        return;
+    }
+    for (; i < n; i += stride) {
+        const float r = f(a[i], b[i]);
+        c[i] = beta != 0.f ? c[i] + r : r;
+    }
+}
+
+// y[i] += x[i]: an adjoint added into a pending buffer (Add's VJP, and the
+// publication of pending into an existing gradient, tensor.rs:341-360).
+__global__ void __launch_bounds__(256) ew_accumulate(const float *__restrict__ x, float *y,
+                                                     int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        y[i] += x[i];
+}
+
+// x[i] = v (fresh zero buffers: a kernel, not a memset, so it can sit in a
+// captured graph).
+__global__ void __launch_bounds__(256) ew_fill(float *x, int64_t n, float v) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = v;
+}
+
+// y[i] += s[0]: Sum's VJP (tensor.rs:410-417) with the scalar adjoint on the
+// device.
+__global__ void __launch_bounds__(256) ew_add_scalar(const float *__restrict__ s, float *y,
+                                                     int64_t n) {
+    const float v = s[0];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        y[i] += v;
+}
+
+// Block sum of one value per thread, in a fixed tree (wave shuffles, then
+// the four wave sums in order).
+__device__ __forceinline__ float block_sum_256(float v) {
+    __shared__ float part[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) part[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    if (threadIdx.x == 0) t = ((part[0] + part[1]) + part[2]) + part[3];
+    __syncthreads();
+    return t;
+}
+
+// Sum, pass 1: block b sums elements [b*chunk, (b+1)*chunk), each thread a
+// strided subsequence in order, then the block tree.
+__global__ void __launch_bounds__(256) sum_partials(const float *__restrict__ x, int64_t n,
+                                                    int64_t chunk, float *part) {
+    const int64_t lo = (int64_t)blockIdx.x * chunk;
+    const int64_t hi = lo + chunk < n ? lo + chunk : n;
+    float v = 0.f;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) v += x[i];
+    const float t = block_sum_256(v);
+    if (threadIdx.x == 0) part[blockIdx.x] = t;
+}
+
+// Sum, pass 2: out[0] = beta*out[0] + sum of the `count` partials, in order
+// per thread, then the block tree.
+__global__ void __launch_bounds__(256) sum_finish(const float *__restrict__ part, int count,
+                                                  float *out, float beta) {
+    float v = 0.f;
+    for (int i = threadIdx.x; i < count; i += 256) v += part[i];
+    const float t = block_sum_256(v);
+    if (threadIdx.x == 0) out[0] = beta != 0.f ? out[0] + t : t;
+}
+
+// out[r] = (sum_h y[r][h]) / hw: one wave per row (the stem's global
+// average pool, N*C rows of OH*OW).
+__global__ void __launch_bounds__(256) mean_rows(const float *__restrict__ y, int64_t rows,
+                                                 int64_t hw, float *out) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *row = y + r * hw;
+    float v = 0.f;
+    for (int64_t i = lane; i < hw; i += 64) v += row[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    if (lane == 0) out[r] = v / (float)hw;
+}
+
+// dy[r][h] = beta*dy[r][h] + g[r]*scale: the mean-pool's VJP.
+__global__ void __launch_bounds__(256) broadcast_rows(const float *__restrict__ g, int64_t rows,
+                                                      int64_t hw, float scale, float *dy,
+                                                      float beta) {
+    const int64_t n = rows * hw;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float v = g[i / hw] * scale;
+        dy[i] = beta != 0.f ? dy[i] + v : v;
+    }
+}
+
+}  // namespace katsu

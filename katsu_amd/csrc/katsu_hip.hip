@@ -12,11 +12,14 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <unordered_map>
 
 #include "../../include/katsu_hip.h"
 #include "igemm.hpp"
 #include "direct.hpp"
+#include "elementwise.hpp"
 
 namespace katsu {
 namespace {
@@ -41,6 +44,13 @@ struct Buffer {
     size_t bytes = 0;
 };
 
+// Device buffers handed out by katsu_hip_malloc: freed blocks are kept for
+// reuse (hipFree synchronises the device) and returned to HIP at shutdown.
+struct Pool {
+    std::multimap<size_t, void *> free;       // block size -> block
+    std::unordered_map<void *, size_t> live;  // block -> size
+};
+
 struct State {
     std::mutex mu;
     bool ready = false;
@@ -48,6 +58,8 @@ struct State {
     hipStream_t stream = nullptr;
     Buffer staging[5];
     Buffer workspace;
+    Buffer sum_scratch;  // partial sums of katsu_hip_sum_f32_dev
+    Pool pool;
 };
 
 State &state() {
@@ -994,6 +1006,59 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
 }
 
 // ---------------------------------------------------------------------------
+// Device engine: buffers and the elementwise kernels.
+
+// Pool block sizes: 512-byte granules below 1 MiB, 2 MiB granules above.
+size_t pool_round(size_t bytes) {
+    const size_t g = bytes < (1u << 20) ? 512 : (2u << 20);
+    return (std::max<size_t>(bytes, 1) + g - 1) / g * g;
+}
+
+int pool_alloc(State &s, size_t bytes, void **out) {
+    const size_t want = pool_round(bytes);
+    auto it = s.pool.free.lower_bound(want);
+    if (it != s.pool.free.end() && it->first <= 2 * want) {
+        *out = it->second;
+        s.pool.live.emplace(it->second, it->first);
+        s.pool.free.erase(it);
+        return KATSU_OK;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        // Return the cached blocks to HIP and try once more.
+        (void)hipGetLastError();
+        for (auto &kv : s.pool.free) (void)hipFree(kv.second);
+        s.pool.free.clear();
+        e = hipMalloc(&p, want);
+        if (e != hipSuccess) return map_hip(e);
+    }
+    s.pool.live.emplace(p, want);
+    *out = p;
+    return KATSU_OK;
+}
+
+// Grid for a streaming kernel over n elements: enough blocks to cover the
+// chip several times over, no more than the work needs.
+unsigned ew_blocks(int64_t n) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, 256), 256 * 16));
+}
+
+template <EwOp OP>
+int ew_binary_launch(const float *a, const float *b, float *c, size_t n, float beta,
+                     hipStream_t st) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    if (n == 0) return KATSU_OK;
+    if (!a || !b || !c) return KATSU_E_INVALID;
+    const int64_t N = (int64_t)n;
+    if (aligned16(a) && aligned16(b) && aligned16(c))
+        ew_binary<OP, true><<<ew_blocks(cdiv(N, 4)), 256, 0, st>>>(a, b, c, N, beta);
+    else
+        ew_binary<OP, false><<<ew_blocks(N), 256, 0, st>>>(a, b, c, N, beta);
+    return launch_status();
+}
+
+// ---------------------------------------------------------------------------
 // Host-pointer wrappers: stage through the pool, run, copy back, synchronise.
 
 int h2d(Buffer &b, const float *src, size_t count, hipStream_t st) {
@@ -1056,6 +1121,11 @@ void katsu_hip_shutdown(void) {
     }
     if (s.workspace.ptr) (void)hipFree(s.workspace.ptr);
     s.workspace = Buffer{};
+    if (s.sum_scratch.ptr) (void)hipFree(s.sum_scratch.ptr);
+    s.sum_scratch = Buffer{};
+    for (auto &kv : s.pool.free) (void)hipFree(kv.second);
+    for (auto &kv : s.pool.live) (void)hipFree(kv.first);
+    s.pool = Pool{};
     (void)hipStreamDestroy(s.stream);
     s.stream = nullptr;
     s.ready = false;
@@ -1252,6 +1322,130 @@ int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,
                              &s.workspace);
     if (rc) return rc;
     return d2h_sync(dw, s.staging[2], nw, s.stream);
+}
+
+void *katsu_hip_stream(void) {
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return init_locked(s) == KATSU_OK ? (void *)s.stream : nullptr;
+}
+
+int katsu_hip_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return KATSU_E_INVALID;
+    *ptr = nullptr;
+    if (bytes == 0) return KATSU_OK;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    int rc = init_locked(s);
+    if (rc) return rc;
+    return pool_alloc(s, bytes, ptr);
+}
+
+int katsu_hip_free(void *ptr) {
+    if (!ptr) return KATSU_OK;
+    State &s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    auto it = s.pool.live.find(ptr);
+    if (it == s.pool.live.end()) return KATSU_E_INVALID;
+    s.pool.free.emplace(it->second, it->first);
+    s.pool.live.erase(it);
+    return KATSU_OK;
+}
+
+int katsu_hip_upload(void *dst, const float *src, size_t count, void *stream) {
+    if (count == 0) return KATSU_OK;
+    if (!dst || !src) return KATSU_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    int rc = map_hip(hipMemcpyAsync(dst, src, count * sizeof(float), hipMemcpyHostToDevice, st));
+    if (rc) return rc;
+    return map_hip(hipStreamSynchronize(st));
+}
+
+int katsu_hip_download(float *dst, const void *src, size_t count, void *stream) {
+    if (count == 0) return KATSU_OK;
+    if (!dst || !src) return KATSU_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    int rc = map_hip(hipMemcpyAsync(dst, src, count * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (rc) return rc;
+    return map_hip(hipStreamSynchronize(st));
+}
+
+int katsu_hip_sync(void *stream) { return map_hip(hipStreamSynchronize((hipStream_t)stream)); }
+
+int katsu_hip_add_f32_dev(const float *a, const float *b, float *c, size_t n, float beta,
+                          void *stream) {
+    return ew_binary_launch<EwOp::Add>(a, b, c, n, beta, (hipStream_t)stream);
+}
+
+int katsu_hip_mul_f32_dev(const float *a, const float *b, float *c, size_t n, float beta,
+                          void *stream) {
+    return ew_binary_launch<EwOp::Mul>(a, b, c, n, beta, (hipStream_t)stream);
+}
+
+int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, void *stream) {
+    if (n == 0) return KATSU_OK;
+    if (!x || !y) return KATSU_E_INVALID;
+    ew_accumulate<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, y, (int64_t)n);
+    return launch_status();
+}
+
+int katsu_hip_fill_f32_dev(float *x, size_t n, float value, void *stream) {
+    if (n == 0) return KATSU_OK;
+    if (!x) return KATSU_E_INVALID;
+    ew_fill<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, (int64_t)n, value);
+    return launch_status();
+}
+
+int katsu_hip_add_scalar_f32_dev(const float *s_, float *y, size_t n, void *stream) {
+    if (n == 0) return KATSU_OK;
+    if (!s_ || !y) return KATSU_E_INVALID;
+    ew_add_scalar<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(s_, y, (int64_t)n);
+    return launch_status();
+}
+
+int katsu_hip_sum_f32_dev(const float *x, size_t n, float *out, float beta, void *stream) {
+    if (!beta_ok(beta) || !out || (n > 0 && !x)) return KATSU_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (n == 0) {  // the empty fold: out = beta*out + 0
+        if (beta == 0.f) ew_fill<<<1, 256, 0, st>>>(out, 1, 0.f);
+        return launch_status();
+    }
+    // A fixed number of chunks for a given n (at most 1024), so the tree is
+    // the same on every call.
+    const int64_t N = (int64_t)n;
+    const int64_t chunk = std::max<int64_t>(4096, cdiv(N, 1024));
+    const int parts = (int)cdiv(N, chunk);
+    State &s = state();
+    float *part;
+    {
+        std::lock_guard<std::mutex> lock(s.mu);
+        int rc = ensure(s.sum_scratch, (size_t)parts * sizeof(float));
+        if (rc) return rc;
+        part = (float *)s.sum_scratch.ptr;
+    }
+    sum_partials<<<parts, 256, 0, st>>>(x, N, chunk, part);
+    sum_finish<<<1, 256, 0, st>>>(part, parts, out, beta);
+    return launch_status();
+}
+
+int katsu_hip_mean_rows_f32_dev(const float *y, size_t rows, size_t cols, float *out,
+                                void *stream) {
+    if (rows == 0) return KATSU_OK;
+    if (!y || !out || cols == 0) return KATSU_E_INVALID;
+    mean_rows<<<(unsigned)cdiv((int64_t)rows, 4), 256, 0, (hipStream_t)stream>>>(
+        y, (int64_t)rows, (int64_t)cols, out);
+    return launch_status();
+}
+
+int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, float scale,
+                                     float *dy, float beta, void *stream) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    if (rows == 0 || cols == 0) return KATSU_OK;
+    if (!g || !dy) return KATSU_E_INVALID;
+    const int64_t n = (int64_t)rows * (int64_t)cols;
+    broadcast_rows<<<ew_blocks(n), 256, 0, (hipStream_t)stream>>>(g, (int64_t)rows,
+                                                                  (int64_t)cols, scale, dy, beta);
+    return launch_status();
 }
 
 }  // extern "C"

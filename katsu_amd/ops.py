@@ -133,3 +133,72 @@ def matmul_vjp(a, b, g, da, db):
     gemm(g, b, m, k, n, trans_b=True, out=da, beta=1.0)
     gemm(a, g, k, n, m, trans_a=True, out=db, beta=1.0)
     return da, db
+
+
+# ---- the device engine's elementwise work (f32, n elements, device tensors) ----
+
+def add(a, b, out=None, beta=0.0):
+    """out = beta*out + (a + b): Tensor::add (tensor.rs:217-240), bit-exact."""
+    _dev_f32(a, b, out)
+    if a.shape != b.shape:
+        raise ValueError("identical shapes required")
+    out = torch.empty_like(a) if out is None else out
+    check(lib().katsu_hip_add_f32_dev(_p(a), _p(b), _p(out), a.numel(), float(beta), _stream()),
+          "add")
+    return out
+
+
+def mul(a, b, out=None, beta=0.0):
+    """out = beta*out + a*b: Tensor::mul, or Mul's VJP with beta = 1."""
+    _dev_f32(a, b, out)
+    if a.shape != b.shape:
+        raise ValueError("identical shapes required")
+    out = torch.empty_like(a) if out is None else out
+    check(lib().katsu_hip_mul_f32_dev(_p(a), _p(b), _p(out), a.numel(), float(beta), _stream()),
+          "mul")
+    return out
+
+
+def accumulate(x, y):
+    """y += x (an adjoint into a pending buffer)."""
+    _dev_f32(x, y)
+    check(lib().katsu_hip_accumulate_f32_dev(_p(x), _p(y), x.numel(), _stream()), "accumulate")
+    return y
+
+
+def fill(x, value):
+    _dev_f32(x)
+    check(lib().katsu_hip_fill_f32_dev(_p(x), x.numel(), float(value), _stream()), "fill")
+    return x
+
+
+def add_scalar(s, y):
+    """y += s[0] (Sum's VJP)."""
+    _dev_f32(s, y)
+    check(lib().katsu_hip_add_scalar_f32_dev(_p(s), _p(y), y.numel(), _stream()), "add_scalar")
+    return y
+
+
+def sum(x, out=None, beta=0.0):
+    """out[0] = beta*out[0] + sum(x): Tensor::sum (tensor.rs:242-247), fixed tree."""
+    _dev_f32(x, out)
+    out = torch.empty(1, device=x.device, dtype=torch.float32) if out is None else out
+    check(lib().katsu_hip_sum_f32_dev(_p(x), x.numel(), _p(out), float(beta), _stream()), "sum")
+    return out
+
+
+def mean_rows(y, rows, cols, out=None):
+    """out[r] = sum_c y[r][c] / cols (the stem chain's global average pool)."""
+    _dev_f32(y, out)
+    out = torch.empty(rows, device=y.device, dtype=torch.float32) if out is None else out
+    check(lib().katsu_hip_mean_rows_f32_dev(_p(y), rows, cols, _p(out), _stream()), "mean_rows")
+    return out
+
+
+def broadcast_rows(g, rows, cols, scale, dy=None, beta=0.0):
+    """dy[r][c] = beta*dy[r][c] + scale*g[r] (the mean pool's VJP)."""
+    _dev_f32(g, dy)
+    dy = torch.empty(rows * cols, device=g.device, dtype=torch.float32) if dy is None else dy
+    check(lib().katsu_hip_broadcast_rows_f32_dev(_p(g), rows, cols, float(scale), _p(dy),
+                                                  float(beta), _stream()), "broadcast_rows")
+    return dy

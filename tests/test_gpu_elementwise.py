@@ -1,0 +1,91 @@
+"""The device engine's elementwise kernels through the C ABI: the ops whose
+reference loops are one rounding per element (add, mul, the VJP
+accumulations, fill, the scalar broadcast) must match numpy's f32 results
+bit for bit, aligned or not, with and without a ragged tail; the reductions
+(sum, row mean) must lie within the f32 summation bound of an exact f64 sum
+and be identical run to run."""
+import numpy as np
+import pytest
+
+from katsu_amd import synth
+from tests.parity import gamma
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [0, 1, 3, 4, 5, 1000, 4099, 1 << 20]
+
+
+def _vec(seed, n):
+    return synth.uniform(seed, (n,)) if n else np.zeros(0, np.float32)
+
+
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_binary_and_accumulate_exact(n, offset, dev):
+    import torch
+
+    from katsu_amd import ops
+    a = _vec(1, n + offset)
+    b = _vec(2, n + offset)
+    c0 = _vec(3, n + offset)
+    ta, tb, tc = (torch.from_numpy(v).to(dev)[offset:] for v in (a, b, c0))  # offset 1: unaligned
+    a, b, c0 = a[offset:], b[offset:], c0[offset:]
+    assert np.array_equal(ops.add(ta, tb).cpu().numpy(), a + b)
+    assert np.array_equal(ops.mul(ta, tb).cpu().numpy(), a * b)
+    out = tc.clone()
+    ops.mul(ta, tb, out=out, beta=1.0)
+    assert np.array_equal(out.cpu().numpy(), c0 + a * b)
+    out = tc.clone()
+    ops.add(ta, tb, out=out, beta=1.0)
+    assert np.array_equal(out.cpu().numpy(), c0 + (a + b))
+    out = tc.clone()
+    ops.accumulate(ta, out)
+    assert np.array_equal(out.cpu().numpy(), c0 + a)
+    out = tc.clone()
+    ops.fill(out, 0.0)
+    assert not out.any()
+    s = torch.tensor([0.25], device=dev)
+    out = tc.clone()
+    ops.add_scalar(s, out)
+    assert np.array_equal(out.cpu().numpy(), c0 + np.float32(0.25))
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 4096, 4097, 1 << 20, 25690112])
+def test_sum_within_bound_and_deterministic(n, dev):
+    import torch
+
+    from katsu_amd import ops
+    x = _vec(5, n)
+    tx = torch.from_numpy(x).to(dev)
+    got = ops.sum(tx).item()
+    again = ops.sum(tx).item()
+    assert got == again
+    exact = float(np.sum(x.astype(np.float64)))
+    # The library's tree: chunks of max(4096, n/1024) elements per block, 256
+    # strided sequential sums per chunk, a 256-lane tree, then the same over
+    # the chunk sums; its longest chain of additions bounds the error.
+    chunk = max(4096, -(-n // 1024))
+    parts = max(1, -(-n // chunk))
+    depth = -(-chunk // 256) + 8 + -(-parts // 256) + 8
+    bound = gamma(depth) * float(np.sum(np.abs(x.astype(np.float64))))
+    assert abs(got - exact) <= bound
+    out = torch.tensor([1.5], device=dev)
+    ops.sum(tx, out=out, beta=1.0)
+    assert abs(out.item() - (1.5 + exact)) <= bound + 2 ** -23 * (1.5 + abs(exact))
+
+
+def test_mean_rows_and_broadcast(dev):
+    import torch
+
+    from katsu_amd import ops
+    rows, cols = 4096, 12544 // 16
+    y = synth.uniform(7, (rows, cols))
+    ty = torch.from_numpy(y).to(dev)
+    m = ops.mean_rows(ty, rows, cols).cpu().numpy()
+    exact = y.astype(np.float64).sum(1) / cols
+    bound = 2 * gamma(cols) * np.abs(y.astype(np.float64)).sum(1) / cols + np.abs(exact) * 2 ** -23
+    assert np.all(np.abs(m - exact) <= bound)
+    g = synth.uniform(8, (rows,))
+    dy = ops.broadcast_rows(torch.from_numpy(g).to(dev), rows, cols, 1.0 / cols).cpu().numpy()
+    assert np.array_equal(dy.reshape(rows, cols), np.repeat((g * np.float32(1.0 / cols))[:, None],
+                                                            cols, 1))
