@@ -305,6 +305,20 @@ def main():
                                "tflops": round(step_flops / (host_ms * 1e-3) / 1e12, 3),
                                "note": "host-pointer ABI, PCIe copies included"}
 
+    # The C++ front end (the reference's public API) with device-resident
+    # tensors: forward + sum + backward through Conv2D at config 3, and
+    # matmul + sum + backward at 1024, end to end (a child process: the
+    # front end's own binary).
+    fb = os.path.join(ROOT, "katsu_amd", "lib", "frontend_bench")
+    if os.path.exists(fb):
+        import subprocess
+        proc = subprocess.run([fb, "--steps", "20"], capture_output=True, text=True, timeout=300)
+        lines = [l for l in proc.stdout.splitlines() if l.startswith("{")]
+        if proc.returncode == 0 and lines:
+            out["frontend_resident"] = json.loads(lines[-1])
+        else:
+            out["frontend_resident"] = {"error": proc.stderr.strip()[-300:]}
+
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
                                            step_flops / cfg["x"][0])

@@ -123,7 +123,10 @@ int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *
  * dx = beta*dx + dX and dw = beta*dw + dW, as the two calls above make them
  * (same results, same determinism).  When both passes take their direct
  * gfx950 kernels they share one launch, so dW work fills the GPU while the
- * last dX tiles finish.  The _dev form takes the workspace of
+ * last dX tiles finish.  dx and dw may be the same buffer (with beta = 1:
+ * an engine's pending buffer when input and weights are one node); dX is
+ * then added before dW, as the reference's adds are ordered
+ * (tensor.rs:383-390).  The _dev form takes the workspace of
  * katsu_hip_conv2d_bwd_filter_workspace (or NULL, as above). */
 int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
                              float *dw, const katsu_conv_geom *g, float beta);
@@ -160,13 +163,14 @@ int katsu_hip_add_f32_dev(const float *a, const float *b, float *c, size_t n, fl
                           void *stream);
 int katsu_hip_mul_f32_dev(const float *a, const float *b, float *c, size_t n, float beta,
                           void *stream);
-/* y += x (Add's VJP, tensor.rs:392-397; publishing pending into an existing
- * gradient, tensor.rs:349-357).  Bit-identical. */
-int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, void *stream);
+/* y = beta*y + x (Add's VJP, tensor.rs:392-397; publishing pending into an
+ * existing gradient, tensor.rs:349-357; beta = 0 copies into a buffer the
+ * caller knows is still zero).  Bit-identical. */
+int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, float beta, void *stream);
 /* x = value (fresh zero buffers, tensor.rs:120-125 and 328-331). */
 int katsu_hip_fill_f32_dev(float *x, size_t n, float value, void *stream);
-/* y += s[0] with s on the device (Sum's VJP, tensor.rs:410-417). */
-int katsu_hip_add_scalar_f32_dev(const float *s, float *y, size_t n, void *stream);
+/* y = beta*y + s[0] with s on the device (Sum's VJP, tensor.rs:410-417). */
+int katsu_hip_add_scalar_f32_dev(const float *s, float *y, size_t n, float beta, void *stream);
 /* out[0] = beta*out[0] + sum(x) (Tensor::sum, tensor.rs:242-247).  A fixed
  * tree, identical run to run; it differs from the reference's sequential
  * fold within the f32 summation bound. */

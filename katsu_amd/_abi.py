@@ -82,9 +82,9 @@ def lib():
         L.katsu_hip_sync.argtypes = [vp]
         L.katsu_hip_add_f32_dev.argtypes = [vp, vp, vp, sz, fp, vp]
         L.katsu_hip_mul_f32_dev.argtypes = [vp, vp, vp, sz, fp, vp]
-        L.katsu_hip_accumulate_f32_dev.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_accumulate_f32_dev.argtypes = [vp, vp, sz, fp, vp]
         L.katsu_hip_fill_f32_dev.argtypes = [vp, sz, fp, vp]
-        L.katsu_hip_add_scalar_f32_dev.argtypes = [vp, vp, sz, vp]
+        L.katsu_hip_add_scalar_f32_dev.argtypes = [vp, vp, sz, fp, vp]
         L.katsu_hip_sum_f32_dev.argtypes = [vp, sz, vp, fp, vp]
         L.katsu_hip_mean_rows_f32_dev.argtypes = [vp, sz, sz, vp, vp]
         L.katsu_hip_broadcast_rows_f32_dev.argtypes = [vp, sz, sz, fp, vp, fp, vp]

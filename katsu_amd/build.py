@@ -3,6 +3,7 @@
   katsu_amd/lib/libkatsu_hip.so   the gfx950 kernels behind the C ABI (hipcc)
   katsu_amd/lib/libkatsu.so       the C++ front end (Tensor/Conv2D mirror of
                                   katsu-core) over that ABI (g++)
+  katsu_amd/lib/frontend_bench    end-to-end steps through the front end
 
 hipcc cross-compiles for gfx950 without a GPU, so this runs in the CPU
 container; the resulting .so files travel with the tree to the GPU box.
@@ -48,6 +49,24 @@ def build_frontend(verbose: bool = False) -> str:
     return FRONTEND_LIB
 
 
+BENCH_SRC = os.path.join(HERE, "cpp", "frontend_bench.cpp")
+BENCH_BIN = os.path.join(LIB_DIR, "frontend_bench")
+
+
+def build_frontend_bench(verbose: bool = False) -> str:
+    """The front end's end-to-end benchmark (run by bench.py)."""
+    tmp = BENCH_BIN + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-Wall", BENCH_SRC, "-o", tmp, "-L", LIB_DIR, "-lkatsu",
+           "-lkatsu_hip", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, BENCH_BIN)
+    return BENCH_BIN
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
@@ -64,6 +83,7 @@ def build(verbose: bool = False) -> str:
         print(err, file=sys.stderr)
     os.replace(tmp, LIB)
     build_frontend(verbose)
+    build_frontend_bench(verbose)
     return LIB
 
 

@@ -8,20 +8,72 @@
 #include <stdexcept>
 #include <unordered_map>
 #include <unordered_set>
+#include <utility>
 
 #include "../../include/katsu_hip.h"
 
 namespace katsu {
 
+// A block of device memory from the library's pool, returned on destruction.
+class DeviceBuf {
+   public:
+    DeviceBuf() = default;
+    DeviceBuf(const DeviceBuf &) = delete;
+    DeviceBuf &operator=(const DeviceBuf &) = delete;
+    DeviceBuf(DeviceBuf &&o) noexcept : p_(std::exchange(o.p_, nullptr)), n_(o.n_) {}
+    DeviceBuf &operator=(DeviceBuf &&o) noexcept {
+        if (this != &o) {
+            release();
+            p_ = std::exchange(o.p_, nullptr);
+            n_ = o.n_;
+        }
+        return *this;
+    }
+    ~DeviceBuf() { release(); }
+    // count floats; a zero count holds no memory.  Returns a katsu_status.
+    int allocate(size_t count) {
+        release();
+        n_ = count;
+        if (count == 0) return KATSU_OK;
+        void *p = nullptr;
+        const int rc = katsu_hip_malloc(&p, count * sizeof(float));
+        p_ = (float *)p;
+        return rc;
+    }
+    float *get() const { return p_; }
+    size_t size() const { return n_; }
+
+   private:
+    void release() {
+        if (p_) (void)katsu_hip_free(p_);
+        p_ = nullptr;
+    }
+    float *p_ = nullptr;
+    size_t n_ = 0;
+};
+
 struct TensorNode {
-    std::vector<float> data;
     std::vector<size_t> shape;
-    // RefCell<Option<Vec<f32>>>: `borrows` counts live GradRef guards.
-    mutable std::optional<std::vector<float>> grad;
+    size_t count = 0;
+    // The data: on the device once uploaded or computed there; on the host
+    // when created from host values or once downloaded.
+    mutable DeviceBuf dev;
+    mutable bool on_device = false;
+    mutable std::optional<std::vector<float>> host;
+    // RefCell<Option<Vec<f32>>>: the gradient lives on the device; `grad_host`
+    // is its downloaded copy, refreshed on grad() after a backward changed
+    // it.  `borrows` counts live GradRef guards.
+    mutable std::optional<DeviceBuf> grad;
+    mutable std::optional<std::vector<float>> grad_host;
+    mutable bool grad_host_stale = false;
     mutable int borrows = 0;
     std::vector<Tensor> parents;
     Op op;
 };
+
+DeviceFault::DeviceFault(int st)
+    : std::runtime_error(std::string("device download failed: ") + katsu_hip_strerror(st)),
+      status(st) {}
 
 namespace {
 
@@ -57,6 +109,25 @@ Result<std::vector<float>> zeros_buffer(size_t count) {
     } catch (const std::length_error &) {
         return err(TensorError::Kind::Allocation);
     }
+}
+
+void *stream() { return katsu_hip_stream(); }
+
+// A device buffer of `count` floats (uninitialised), or Device/Allocation.
+Result<DeviceBuf> device_buffer(size_t count) {
+    DeviceBuf b;
+    const int rc = b.allocate(count);
+    if (rc == KATSU_E_OOM) return err(TensorError::Kind::Allocation);
+    if (rc != KATSU_OK) return device(rc);
+    return b;
+}
+
+// A zero-filled device buffer (zeros_buffer, tensor.rs:120-125, on the GPU).
+Result<DeviceBuf> device_zeros(size_t count) {
+    KATSU_TRY(b, device_buffer(count));
+    const int rc = katsu_hip_fill_f32_dev(b.get(), count, 0.0f, stream());
+    if (rc != KATSU_OK) return device(rc);
+    return b;
 }
 
 bool checked_mul(size_t a, size_t b, size_t *out) { return !__builtin_mul_overflow(a, b, out); }
@@ -108,7 +179,7 @@ GradRef::GradRef(const TensorNode *n) : node_(n) { ++node_->borrows; }
 GradRef::~GradRef() {
     if (node_) --node_->borrows;
 }
-const std::optional<std::vector<float>> &GradRef::operator*() const { return node_->grad; }
+const std::optional<std::vector<float>> &GradRef::operator*() const { return node_->grad_host; }
 
 // ---------------------------------------------------------------------------
 // Tensor.
@@ -116,12 +187,30 @@ const std::optional<std::vector<float>> &GradRef::operator*() const { return nod
 Tensor Tensor::node(std::vector<float> data, std::vector<size_t> shape, Op op,
                     std::vector<Tensor> parents) {
     auto n = std::make_shared<TensorNode>();
-    n->data = std::move(data);
+    n->count = data.size();
+    n->host = std::move(data);
     n->shape = std::move(shape);
     n->op = op;
     n->parents = std::move(parents);
     return Tensor(std::move(n));
 }
+
+namespace {
+// A node whose data was computed on the device.
+Tensor device_node(DeviceBuf data, std::vector<size_t> shape, Op op, std::vector<Tensor> parents,
+                   size_t count) {
+    auto n = std::make_shared<TensorNode>();
+    n->count = count;
+    n->dev = std::move(data);
+    n->on_device = true;
+    n->shape = std::move(shape);
+    n->op = op;
+    n->parents = std::move(parents);
+    return Tensor::from_node(std::move(n));
+}
+}  // namespace
+
+Tensor Tensor::from_node(std::shared_ptr<TensorNode> n) { return Tensor(std::move(n)); }
 
 // tensor.rs:149-158.
 Result<Tensor> Tensor::create(std::vector<float> data, const std::vector<size_t> &shape) {
@@ -138,14 +227,48 @@ Result<Tensor> Tensor::zeros(const std::vector<size_t> &shape) {
 }
 
 const std::vector<size_t> &Tensor::shape() const { return node_->shape; }
-const std::vector<float> &Tensor::data() const { return node_->data; }
+size_t Tensor::numel() const { return node_->count; }
+
+const std::vector<float> &Tensor::data() const {
+    TensorNode &n = *node_;
+    if (!n.host) {
+        std::vector<float> h(n.count);
+        const int rc = katsu_hip_download(h.data(), n.dev.get(), n.count, stream());
+        if (rc != KATSU_OK) throw DeviceFault(rc);
+        n.host = std::move(h);
+    }
+    return *n.host;
+}
+
+Result<const float *> Tensor::device_data() const {
+    TensorNode &n = *node_;
+    if (!n.on_device) {
+        KATSU_TRY(b, device_buffer(n.count));
+        const int rc = katsu_hip_upload(b.get(), n.host->data(), n.count, stream());
+        if (rc != KATSU_OK) return device(rc);
+        n.dev = std::move(b);
+        n.on_device = true;
+    }
+    return (const float *)n.dev.get();
+}
+
 Op Tensor::op() const { return node_->op; }
 const std::vector<Tensor> &Tensor::parents() const { return node_->parents; }
 
 // tensor.rs:199-205: fails while the engine holds the gradient mutably
-// (which it never does between calls in this single-threaded mirror).
+// (which it never does between calls in this single-threaded mirror).  The
+// device gradient is downloaded here when a backward has changed it.
 Result<GradRef> Tensor::grad() const {
-    if (node_->borrows < 0) return err(TensorError::Kind::GradientBorrowed);
+    TensorNode &n = *node_;
+    if (n.borrows < 0) return err(TensorError::Kind::GradientBorrowed);
+    if (n.grad_host_stale) {
+        if (n.borrows != 0) return err(TensorError::Kind::GradientBorrowed);
+        std::vector<float> h(n.grad->size());
+        const int rc = katsu_hip_download(h.data(), n.grad->get(), h.size(), stream());
+        if (rc != KATSU_OK) return device(rc);
+        n.grad_host = std::move(h);
+        n.grad_host_stale = false;
+    }
     return GradRef(node_.get());
 }
 
@@ -153,31 +276,38 @@ Result<GradRef> Tensor::grad() const {
 Status Tensor::zero_grad() const {
     if (node_->borrows != 0) return err(TensorError::Kind::GradientBorrowed);
     node_->grad.reset();
+    node_->grad_host.reset();
+    node_->grad_host_stale = false;
     return Unit{};
 }
 
 Result<Tensor> Tensor::add(const Tensor &rhs) const { return elementwise(rhs, Op::Kind::Add); }
 Result<Tensor> Tensor::mul(const Tensor &rhs) const { return elementwise(rhs, Op::Kind::Mul); }
 
-// tensor.rs:226-240: identical shapes, no broadcasting.
+// tensor.rs:226-240: identical shapes, no broadcasting; on the GPU.
 Result<Tensor> Tensor::elementwise(const Tensor &rhs, Op::Kind op) const {
     if (shape() != rhs.shape()) return err(TensorError::Kind::ShapeMismatch);
-    KATSU_TRY(out, zeros_buffer(numel()));
-    const float *a = data().data(), *b = rhs.data().data();
-    for (size_t i = 0; i < out.size(); ++i) out[i] = op == Op::Kind::Add ? a[i] + b[i] : a[i] * b[i];
-    return node(std::move(out), shape(), Op{op}, {*this, rhs});
+    KATSU_TRY(a, device_data());
+    KATSU_TRY(b, rhs.device_data());
+    KATSU_TRY(out, device_buffer(numel()));
+    const int rc = op == Op::Kind::Add
+                       ? katsu_hip_add_f32_dev(a, b, out.get(), numel(), 0.0f, stream())
+                       : katsu_hip_mul_f32_dev(a, b, out.get(), numel(), 0.0f, stream());
+    if (rc != KATSU_OK) return device(rc);
+    return device_node(std::move(out), shape(), Op{op}, {*this, rhs}, numel());
 }
 
-// tensor.rs:242-247: a sequential f32 fold (0 for an empty tensor).
+// tensor.rs:242-247: the sum of all elements (0 for an empty tensor), on the
+// GPU in a fixed tree.
 Result<Tensor> Tensor::sum() const {
-    KATSU_TRY(out, zeros_buffer(1));
-    float acc = 0.0f;
-    for (float v : data()) acc += v;
-    out[0] = acc;
-    return node(std::move(out), {}, Op{Op::Kind::Sum}, {*this});
+    KATSU_TRY(x, device_data());
+    KATSU_TRY(out, device_buffer(1));
+    const int rc = katsu_hip_sum_f32_dev(x, numel(), out.get(), 0.0f, stream());
+    if (rc != KATSU_OK) return device(rc);
+    return device_node(std::move(out), {}, Op{Op::Kind::Sum}, {*this}, 1);
 }
 
-// tensor.rs:249-280, seam S1: the product runs on the GPU.
+// tensor.rs:249-280, seam S1.
 Result<Tensor> Tensor::matmul(const Tensor &rhs) const {
     if (rank() != 2 || rhs.rank() != 2) {
         TensorError e{TensorError::Kind::RankMismatch};
@@ -193,13 +323,13 @@ Result<Tensor> Tensor::matmul(const Tensor &rhs) const {
         return e;
     }
     KATSU_TRY(count, element_count({m, n}));
-    KATSU_TRY(out, zeros_buffer(count));
-    if (!out.empty() && k != 0) {
-        const int rc = katsu_hip_gemm_f32(data().data(), rhs.data().data(), out.data(), m, n, k,
-                                          0, 0, 0.0f);
-        if (rc != KATSU_OK) return device(rc);
-    }
-    return node(std::move(out), {m, n}, Op{Op::Kind::Matmul}, {*this, rhs});
+    KATSU_TRY(a, device_data());
+    KATSU_TRY(b, rhs.device_data());
+    KATSU_TRY(out, device_buffer(count));
+    // beta = 0 writes every element; k == 0 gives the zero buffer of :264.
+    const int rc = katsu_hip_gemm_f32_dev(a, b, out.get(), m, n, k, 0, 0, 0.0f, stream());
+    if (rc != KATSU_OK) return device(rc);
+    return device_node(std::move(out), {m, n}, Op{Op::Kind::Matmul}, {*this, rhs}, count);
 }
 
 // tensor.rs:286-306: iterative DFS, parents before children, deduplicated
@@ -230,64 +360,97 @@ Status Tensor::backward() const {
 }
 
 namespace {
-Result<std::pair<std::vector<float>, std::vector<float>>> backward_buffers(
-    const Tensor &input, const Tensor &weights, const std::vector<float> &grad, size_t stride,
-    size_t padding);
+Result<katsu_conv_geom> geometry(const Tensor &input, const Tensor &weights, size_t stride,
+                                 size_t padding);
 }  // namespace
 
 struct Engine {
-    using Pending = std::unordered_map<const TensorNode *, std::vector<float>>;
+    // The adjoint buffer of one node in one backward pass, on the device.
+    // `zero` marks a buffer that no adjoint has reached yet: it holds no
+    // values, and the first adjoint is written into it (beta = 0) instead of
+    // added to a zero fill, which saves a fill and a read of every buffer.
+    struct Slot {
+        DeviceBuf buf;
+        bool zero = true;
+        float beta() const { return zero ? 0.0f : 1.0f; }
+    };
+    using Pending = std::unordered_map<const TensorNode *, Slot>;
 
-    // Op::backward, tensor.rs:365-449.
-    static Status op_backward(const Tensor &node, const std::vector<float> &g, Pending &pending) {
+    // Op::backward, tensor.rs:365-449: every adjoint accumulated into the
+    // device pending buffers in the reference's order.
+    static Status op_backward(const Tensor &node, const float *g, Pending &pending) {
         const Op op = node.op();
         const auto &ps = node.parents();
+        void *st = stream();
+        auto slot = [&](int side) -> Slot & { return pending.at(ps[side].node_.get()); };
+        int rc = KATSU_OK;
         switch (op.kind) {
             case Op::Kind::Leaf: break;
             case Op::Kind::Conv2D: {
-                // tensor.rs:374-391, seam S4: fresh dx, dw from the GPU, then
-                // added into the pending buffers one parent after the other.
-                KATSU_TRY(grads, backward_buffers(ps[0], ps[1], g, op.stride, op.padding));
-                const std::vector<float> *both[2] = {&grads.first, &grads.second};
-                for (int side = 0; side < 2; ++side) {
-                    std::vector<float> &target = pending.at(ps[side].node_.get());
-                    const std::vector<float> &src = *both[side];
-                    for (size_t i = 0; i < target.size() && i < src.size(); ++i) target[i] += src[i];
+                // tensor.rs:374-391, seam S4: dx into pending[input], then dw into
+                // pending[weights], each fresh adjoint added once as the
+                // reference's += of the fresh buffers does.
+                KATSU_TRY(geo, geometry(ps[0], ps[1], op.stride, op.padding));
+                KATSU_TRY(x, ps[0].device_data());
+                KATSU_TRY(w, ps[1].device_data());
+                Slot &sx = slot(0), &sw = slot(1);
+                if (&sx != &sw && sx.zero == sw.zero) {
+                    rc = katsu_hip_conv2d_bwd_f32_dev(x, w, g, sx.buf.get(), sw.buf.get(), &geo,
+                                                      sx.beta(), nullptr, 0, st);
+                } else {
+                    rc = katsu_hip_conv2d_bwd_data_f32_dev(g, w, sx.buf.get(), &geo, sx.beta(), st);
+                    sx.zero = false;
+                    if (rc == KATSU_OK)
+                        rc = katsu_hip_conv2d_bwd_filter_f32_dev(x, g, sw.buf.get(), &geo,
+                                                                 sw.beta(), nullptr, 0, st);
                 }
+                sx.zero = sw.zero = false;
                 break;
             }
             case Op::Kind::Add:
+                // tensor.rs:392-397: both edges, even when they are one node.
+                for (int side = 0; side < 2 && rc == KATSU_OK; ++side) {
+                    Slot &t = slot(side);
+                    rc = katsu_hip_accumulate_f32_dev(g, t.buf.get(), node.numel(), t.beta(), st);
+                    t.zero = false;
+                }
+                break;
             case Op::Kind::Mul:
-                // tensor.rs:392-409: both edges, even when they are one node.
-                for (int side = 0; side < 2; ++side) {
-                    std::vector<float> &target = pending.at(ps[side].node_.get());
-                    const std::vector<float> &other = ps[1 - side].data();
-                    for (size_t i = 0; i < target.size() && i < g.size(); ++i)
-                        target[i] += op.kind == Op::Kind::Add ? g[i] : g[i] * other[i];
+                // tensor.rs:398-409: pending[side] += g * other.
+                for (int side = 0; side < 2 && rc == KATSU_OK; ++side) {
+                    KATSU_TRY(other, ps[1 - side].device_data());
+                    Slot &t = slot(side);
+                    rc = katsu_hip_mul_f32_dev(g, other, t.buf.get(), node.numel(), t.beta(), st);
+                    t.zero = false;
                 }
                 break;
             case Op::Kind::Sum: {
                 // tensor.rs:410-417.
-                for (float &v : pending.at(ps[0].node_.get())) v += g[0];
+                Slot &t = slot(0);
+                rc = katsu_hip_add_scalar_f32_dev(g, t.buf.get(), ps[0].numel(), t.beta(), st);
+                t.zero = false;
                 break;
             }
             case Op::Kind::Matmul: {
-                // tensor.rs:418-445, seam S2: dA += G.B^T, then dB += A^T.G, on
-                // the GPU with beta = 1 into the pending buffers (the same
-                // buffer when A and B are one node, hence the order).
+                // tensor.rs:418-445, seam S2: dA += G.B^T, then dB += A^T.G, into
+                // the pending buffers (the same buffer when A and B are one
+                // node, hence the order).
                 const Tensor &a = ps[0], &b = ps[1];
                 const size_t m = a.shape()[0], k = a.shape()[1], n = b.shape()[1];
-                if (g.empty() || k == 0) break;
-                std::vector<float> &da = pending.at(a.node_.get());
-                int rc = katsu_hip_gemm_f32(g.data(), b.data().data(), da.data(), m, k, n, 0, 1,
-                                            1.0f);
-                if (rc != KATSU_OK) return device(rc);
-                std::vector<float> &db = pending.at(b.node_.get());
-                rc = katsu_hip_gemm_f32(a.data().data(), g.data(), db.data(), k, n, m, 1, 0, 1.0f);
-                if (rc != KATSU_OK) return device(rc);
+                if (node.numel() == 0 || k == 0) break;
+                KATSU_TRY(ad, a.device_data());
+                KATSU_TRY(bd, b.device_data());
+                Slot &sa = slot(0);
+                rc = katsu_hip_gemm_f32_dev(g, bd, sa.buf.get(), m, k, n, 0, 1, sa.beta(), st);
+                sa.zero = false;
+                Slot &sb = slot(1);
+                if (rc == KATSU_OK)
+                    rc = katsu_hip_gemm_f32_dev(ad, g, sb.buf.get(), k, n, m, 1, 0, sb.beta(), st);
+                sb.zero = false;
                 break;
             }
         }
+        if (rc != KATSU_OK) return device(rc);
         return Unit{};
     }
 };
@@ -297,31 +460,45 @@ struct Engine {
 Status Tensor::backward_with(const std::vector<float> &seed) const {
     if (seed.size() != numel()) return data_length(numel(), seed.size());
     const std::vector<Tensor> order = topological_order();
+    void *st = stream();
     Engine::Pending pending;
     for (const Tensor &n : order) {
-        KATSU_TRY(buf, zeros_buffer(n.numel()));
-        pending.emplace(n.node_.get(), std::move(buf));
+        KATSU_TRY(buf, device_buffer(n.numel()));
+        pending.emplace(n.node_.get(), Engine::Slot{std::move(buf), true});
     }
-    pending.at(node_.get()) = seed;
+    {
+        // A one-element seed (backward()) is written by a kernel, so the pass
+        // never waits on the host; longer seeds are copied in.
+        Engine::Slot &root = pending.at(node_.get());
+        const int rc = seed.size() == 1
+                           ? katsu_hip_fill_f32_dev(root.buf.get(), 1, seed[0], st)
+                           : katsu_hip_upload(root.buf.get(), seed.data(), seed.size(), st);
+        if (rc != KATSU_OK) return device(rc);
+        root.zero = false;
+    }
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
-        const TensorNode *id = it->node_.get();
-        std::vector<float> upstream = std::move(pending.at(id));
-        pending.erase(id);
-        Status st = Engine::op_backward(*it, upstream, pending);
-        if (!st.ok()) return st;
-        pending.emplace(id, std::move(upstream));
+        Engine::Slot &up = pending.at(it->node_.get());
+        if (up.zero) {  // no adjoint reached this node: its upstream is zeros
+            const int rc = katsu_hip_fill_f32_dev(up.buf.get(), it->numel(), 0.0f, st);
+            if (rc != KATSU_OK) return device(rc);
+            up.zero = false;
+        }
+        Status s = Engine::op_backward(*it, up.buf.get(), pending);
+        if (!s.ok()) return s;
     }
     for (const Tensor &n : order)
         if (n.node_->borrows != 0) return err(TensorError::Kind::GradientBorrowed);
     for (const Tensor &n : order) {
-        std::vector<float> &gradient = pending.at(n.node_.get());
+        DeviceBuf &gradient = pending.at(n.node_.get()).buf;
         auto &stored = n.node_->grad;
         if (stored) {
-            for (size_t i = 0; i < stored->size() && i < gradient.size(); ++i)
-                (*stored)[i] += gradient[i];
+            const int rc =
+                katsu_hip_accumulate_f32_dev(gradient.get(), stored->get(), n.numel(), 1.0f, st);
+            if (rc != KATSU_OK) return device(rc);
         } else {
             stored = std::move(gradient);
         }
+        n.node_->grad_host_stale = true;
     }
     return Unit{};
 }
@@ -376,17 +553,21 @@ Result<katsu_conv_geom> geometry(const Tensor &input, const Tensor &weights, siz
 }
 
 // backward_buffers, conv2d.rs:269-292, seam S4: fresh dx and dw, both from
-// the GPU in one call (beta = 0).
-Result<std::pair<std::vector<float>, std::vector<float>>> backward_buffers(
-    const Tensor &input, const Tensor &weights, const std::vector<float> &grad, size_t stride,
-    size_t padding) {
+// the GPU in one call (beta = 0), kept on the device.
+Result<std::pair<DeviceBuf, DeviceBuf>> backward_buffers(const Tensor &input,
+                                                         const Tensor &weights,
+                                                         const Tensor &grad, size_t stride,
+                                                         size_t padding) {
     KATSU_TRY(g, geometry(input, weights, stride, padding));
     KATSU_TRY(expected, element_count({g.n, g.k, g.oh, g.ow}));
-    if (grad.size() != expected) return data_length(expected, grad.size());
-    KATSU_TRY(dx, zeros_buffer(input.numel()));
-    KATSU_TRY(dw, zeros_buffer(weights.numel()));
-    const int rc = katsu_hip_conv2d_bwd_f32(input.data().data(), weights.data().data(),
-                                            grad.data(), dx.data(), dw.data(), &g, 0.0f);
+    if (grad.numel() != expected) return data_length(expected, grad.numel());
+    KATSU_TRY(x, input.device_data());
+    KATSU_TRY(w, weights.device_data());
+    KATSU_TRY(gy, grad.device_data());
+    KATSU_TRY(dx, device_buffer(input.numel()));
+    KATSU_TRY(dw, device_buffer(weights.numel()));
+    const int rc = katsu_hip_conv2d_bwd_f32_dev(x, w, gy, dx.get(), dw.get(), &g, 0.0f, nullptr,
+                                                0, stream());
     if (rc != KATSU_OK) return device(rc);
     return std::make_pair(std::move(dx), std::move(dw));
 }
@@ -443,14 +624,13 @@ Result<Tensor> Conv2D::forward(const Tensor &input) const {
     KATSU_TRY(g, geometry(input, weights_, stride_, padding_));
     const std::vector<size_t> shape{g.n, g.k, g.oh, g.ow};
     KATSU_TRY(count, element_count(shape));
-    KATSU_TRY(data, zeros_buffer(count));
-    if (!data.empty()) {
-        const int rc = katsu_hip_conv2d_fwd_f32(input.data().data(), weights_.data().data(),
-                                                data.data(), &g);
-        if (rc != KATSU_OK) return device(rc);
-    }
+    KATSU_TRY(x, input.device_data());
+    KATSU_TRY(w, weights_.device_data());
+    KATSU_TRY(y, device_buffer(count));
+    const int rc = katsu_hip_conv2d_fwd_f32_dev(x, w, y.get(), &g, stream());
+    if (rc != KATSU_OK) return device(rc);
     Op op{Op::Kind::Conv2D, stride_, padding_};
-    Tensor out = Tensor::node(std::move(data), shape, op, {input, weights_});
+    Tensor out = device_node(std::move(y), shape, op, {input, weights_}, count);
     *last_forward_ = std::make_pair(input, out);
     return out;
 }
@@ -461,9 +641,9 @@ Result<std::pair<Tensor, Tensor>> Conv2D::backward(const Tensor &grad_output) co
     const auto &[input, output] = **last_forward_;
     if (grad_output.shape() != output.shape())
         return invalid_conv("grad_output must match the output NCHW shape");
-    KATSU_TRY(bufs, backward_buffers(input, weights_, grad_output.data(), stride_, padding_));
-    KATSU_TRY(dx, Tensor::create(std::move(bufs.first), input.shape()));
-    KATSU_TRY(dw, Tensor::create(std::move(bufs.second), weights_.shape()));
+    KATSU_TRY(bufs, backward_buffers(input, weights_, grad_output, stride_, padding_));
+    Tensor dx = device_node(std::move(bufs.first), input.shape(), Op{}, {}, input.numel());
+    Tensor dw = device_node(std::move(bufs.second), weights_.shape(), Op{}, {}, weights_.numel());
     return std::make_pair(dx, dw);
 }
 

@@ -15,23 +15,36 @@
 // keywords or conventions: `Tensor::new` is `Tensor::create`, `Conv2D::new`
 // is `Conv2D::create`.
 //
-// The matmul, its VJPs and both convolution passes run on the GPU (host
-// buffers in, host buffers out, as the reference's slices are); the
-// elementwise ops, sum and the graph bookkeeping stay on the host, as in
-// the reference.  A device failure is reported as TensorError::Device, a
-// variant the reference lacks (it has no device).
+// Tensor data lives on the GPU.  A tensor made from host data (create,
+// zeros, the seeded weights) keeps that host copy and uploads it on its first
+// use by a kernel; every op result, adjoint and gradient is produced and kept
+// in device memory, and data() / grad() download it on first access (node
+// data is immutable, tensor.rs:96, so the host copy never goes stale).  The
+// matmul and its VJPs, both convolution passes, the elementwise ops, sum,
+// their VJPs, and the engine's pending buffers all run on the GPU through the
+// C ABI; only shape checks and graph bookkeeping stay on the host.  A device
+// failure is reported as TensorError::Device, a variant the reference lacks
+// (it has no device); data(), which cannot return an error, throws
+// katsu::DeviceFault if its download fails.
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
 #include <memory>
 #include <optional>
+#include <stdexcept>
 #include <string>
 #include <utility>
 #include <variant>
 #include <vector>
 
 namespace katsu {
+
+// Thrown by Tensor::data() when the download of a device result fails.
+struct DeviceFault : std::runtime_error {
+    int status;
+    explicit DeviceFault(int st);
+};
 
 // tensor.rs:9-30, plus Device for a failed library call.
 struct TensorError {
@@ -119,9 +132,13 @@ class Tensor {
     static Result<Tensor> zeros(const std::vector<size_t> &shape);
 
     const std::vector<size_t> &shape() const;
+    // The values (downloaded from the device on first access).
     const std::vector<float> &data() const;
     size_t rank() const { return shape().size(); }
-    size_t numel() const { return data().size(); }
+    size_t numel() const;
+    // The device copy of the data (uploading host data on first use), or a
+    // Device error; null for an empty tensor.  Valid while the node lives.
+    Result<const float *> device_data() const;
     Op op() const;
     const std::vector<Tensor> &parents() const;
 
@@ -138,9 +155,10 @@ class Tensor {
 
     bool same_node(const Tensor &o) const { return node_ == o.node_; }
 
-    // Crate-internal (Tensor::node, tensor.rs:182-190).
+    // Crate-internal (Tensor::node, tensor.rs:182-190), and its device form.
     static Tensor node(std::vector<float> data, std::vector<size_t> shape, Op op,
                        std::vector<Tensor> parents);
+    static Tensor from_node(std::shared_ptr<TensorNode> n);
 
    private:
     explicit Tensor(std::shared_ptr<TensorNode> n) : node_(std::move(n)) {}

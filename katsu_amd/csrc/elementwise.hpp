@@ -54,13 +54,14 @@ __global__ void __launch_bounds__(256) ew_binary(const float *__restrict__ a,
     }
 }
 
-// y[i] += x[i]: an adjoint added into a pending buffer (Add's VJP, and the
-// publication of pending into an existing gradient, tensor.rs:341-360).
+// y[i] = beta*y[i] + x[i]: an adjoint added into a pending buffer (Add's VJP,
+// and the publication of pending into an existing gradient,
+// tensor.rs:341-360); beta = 0 copies into a buffer still known to be zero.
 __global__ void __launch_bounds__(256) ew_accumulate(const float *__restrict__ x, float *y,
-                                                     int64_t n) {
+                                                     int64_t n, float beta) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        y[i] += x[i];
+        y[i] = beta != 0.f ? y[i] + x[i] : x[i];
 }
 
 // x[i] = v (fresh zero buffers: a kernel, not a memset, so it can sit in a
@@ -70,14 +71,14 @@ __global__ void __launch_bounds__(256) ew_fill(float *x, int64_t n, float v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = v;
 }
 
-// y[i] += s[0]: Sum's VJP (tensor.rs:410-417) with the scalar adjoint on the
-// device.
+// y[i] = beta*y[i] + s[0]: Sum's VJP (tensor.rs:410-417) with the scalar
+// adjoint on the device.
 __global__ void __launch_bounds__(256) ew_add_scalar(const float *__restrict__ s, float *y,
-                                                     int64_t n) {
+                                                     int64_t n, float beta) {
     const float v = s[0];
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        y[i] += v;
+        y[i] = beta != 0.f ? y[i] + v : v;
 }
 
 // Block sum of one value per thread, in a fixed tree (wave shuffles, then

@@ -979,11 +979,14 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     ConvDims d;
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
-    if (!dx || !dw) return KATSU_E_INVALID;
+    if (!dw || (d.npix_in > 0 && !dx)) return KATSU_E_INVALID;
     DirectFwdProblem P;
     DirectFwdPlan xp;
     DwPlan wpl;
-    const bool fused = d.npix_out > 0 && x && w && gy && dx_as_forward(d, gy, w, dx, beta, &P) &&
+    // One output buffer for both (an engine's pending buffer when input and
+    // weights are one node): the two passes run one after the other.
+    const bool fused = dx != dw && d.npix_out > 0 && x && w && gy &&
+                       dx_as_forward(d, gy, w, dx, beta, &P) &&
                        P.CO >= FwdV::KT && direct_fwd_plan<KATSU_FWD_VARIANT, 1>(P, &xp) &&
                        (wpl = dw_plan_any(d)).direct.ok && dw_variant_fusable(wpl.direct.variant);
     if (!fused) {
@@ -1382,10 +1385,13 @@ int katsu_hip_mul_f32_dev(const float *a, const float *b, float *c, size_t n, fl
     return ew_binary_launch<EwOp::Mul>(a, b, c, n, beta, (hipStream_t)stream);
 }
 
-int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, void *stream) {
+int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, float beta,
+                                 void *stream) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
     if (n == 0) return KATSU_OK;
     if (!x || !y) return KATSU_E_INVALID;
-    ew_accumulate<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, y, (int64_t)n);
+    ew_accumulate<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, y, (int64_t)n,
+                                                                          beta);
     return launch_status();
 }
 
@@ -1396,10 +1402,13 @@ int katsu_hip_fill_f32_dev(float *x, size_t n, float value, void *stream) {
     return launch_status();
 }
 
-int katsu_hip_add_scalar_f32_dev(const float *s_, float *y, size_t n, void *stream) {
+int katsu_hip_add_scalar_f32_dev(const float *s_, float *y, size_t n, float beta,
+                                 void *stream) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
     if (n == 0) return KATSU_OK;
     if (!s_ || !y) return KATSU_E_INVALID;
-    ew_add_scalar<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(s_, y, (int64_t)n);
+    ew_add_scalar<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(s_, y, (int64_t)n,
+                                                                          beta);
     return launch_status();
 }
 

@@ -159,10 +159,11 @@ def mul(a, b, out=None, beta=0.0):
     return out
 
 
-def accumulate(x, y):
-    """y += x (an adjoint into a pending buffer)."""
+def accumulate(x, y, beta=1.0):
+    """y = beta*y + x (an adjoint into a pending buffer)."""
     _dev_f32(x, y)
-    check(lib().katsu_hip_accumulate_f32_dev(_p(x), _p(y), x.numel(), _stream()), "accumulate")
+    check(lib().katsu_hip_accumulate_f32_dev(_p(x), _p(y), x.numel(), float(beta), _stream()),
+          "accumulate")
     return y
 
 
@@ -172,10 +173,11 @@ def fill(x, value):
     return x
 
 
-def add_scalar(s, y):
-    """y += s[0] (Sum's VJP)."""
+def add_scalar(s, y, beta=1.0):
+    """y = beta*y + s[0] (Sum's VJP)."""
     _dev_f32(s, y)
-    check(lib().katsu_hip_add_scalar_f32_dev(_p(s), _p(y), y.numel(), _stream()), "add_scalar")
+    check(lib().katsu_hip_add_scalar_f32_dev(_p(s), _p(y), y.numel(), float(beta), _stream()),
+          "add_scalar")
     return y
 
 

@@ -1,9 +1,9 @@
 """The reference's 19 integration tests, ported onto the C++ front end
 (katsu_amd/cpp) and run by the driver tests/cpp/_build/test_frontend.
 
-Tests that reach a matmul or convolution kernel need the GPU; the others
-(shape validation, errors, elementwise autograd, empty problems) run
-anywhere.  The driver is run once per session; each test checks its line."""
+The front end keeps tensor data, adjoints and gradients on the GPU, so every
+test that computes needs it; the shape-validation tests run anywhere.  The
+driver is run once per session; each test checks its line."""
 import os
 import subprocess
 import sys
@@ -13,21 +13,22 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DRIVER = os.path.join(ROOT, "tests", "cpp", "_build", "test_frontend")
 
-# No kernel launch: runnable without a GPU.
+# No kernel launch (shape and length validation only): runnable without a GPU.
 HOST_ONLY = [
     "validates_data_and_storage_size",
     "scalar_and_empty_shapes",
-    "addition_preserves_inputs",
     "rejects_invalid_matmul",
+]
+# Compute on the GPU: every op, adjoint and gradient of the front end is
+# device-resident.
+DEVICE = [
+    "addition_preserves_inputs",
     "empty_matmul_and_output_overflow",
     "squared_error_shared_nodes_and_repeated_backward",
     "diamond_and_clone_identity",
     "explicit_seed_and_errors_are_atomic",
     "empty_graph_operations",
     "empty_batch_and_seeded_initialization",
-]
-# Reach the gfx950 kernels through the C ABI.
-DEVICE = [
     "rectangular_matmul",
     "matmul_finite_differences",
     "matmul_same_parent_accumulates_both_edges",

@@ -41,6 +41,8 @@ def test_binary_and_accumulate_exact(n, offset, dev):
     out = tc.clone()
     ops.accumulate(ta, out)
     assert np.array_equal(out.cpu().numpy(), c0 + a)
+    ops.accumulate(ta, out, beta=0.0)
+    assert np.array_equal(out.cpu().numpy(), a)
     out = tc.clone()
     ops.fill(out, 0.0)
     assert not out.any()
@@ -48,6 +50,8 @@ def test_binary_and_accumulate_exact(n, offset, dev):
     out = tc.clone()
     ops.add_scalar(s, out)
     assert np.array_equal(out.cpu().numpy(), c0 + np.float32(0.25))
+    ops.add_scalar(s, out, beta=0.0)
+    assert np.array_equal(out.cpu().numpy(), np.full(n, 0.25, np.float32))
 
 
 @pytest.mark.parametrize("n", [0, 1, 7, 4096, 4097, 1 << 20, 25690112])
