@@ -4,6 +4,8 @@
 //   conv:   y = layer.forward(x); y.sum().backward()   (config 3: the upstream
 //           gradient of sum() is all-ones, as the benchmark config states)
 //   matmul: c = a.matmul(b);     c.sum().backward()    (config 2, n = 1024)
+//   stem:   the config-5 chain: stem conv, mean pool, matmul head, sum,
+//           backward, spread of dP over HW, backward of the stem
 //
 // Inputs are created from host values once; every step leaves x.grad and the
 // weights' gradient on the device (zero_grad between steps), so no step
@@ -100,12 +102,45 @@ int main(int argc, char **argv) {
     const double mm_ms = (now() - t0) / steps * 1e3;
     const double mm_flop = 3.0 * 2.0 * n * n * n;
 
+    // Config 5: the stem and its head.  y = conv(x) [64,64,112,112]; P = mean
+    // over HW; L = sum(P . H) with H [64,1000]; backward into P; dY = dP/HW
+    // spread over HW; y.backward_with(dY) gives dX and dW.
+    Tensor xs = must(Tensor::create(uniform(1, 64 * 3 * 224 * 224), {64, 3, 224, 224}), "x5");
+    Tensor ws = must(Tensor::create(uniform(2, 64 * 3 * 49), {64, 3, 7, 7}), "w5");
+    Tensor hs = must(Tensor::create(uniform(4, 64 * 1000), {64, 1000}), "h5");
+    Conv2D stem = must(Conv2D::from_weights(ws, 2, 3), "stem");
+    auto stem_step = [&]() {
+        Tensor y = must(stem.forward(xs), "stem forward");
+        Tensor pooled = must(mean_pool_hw(y), "pool");
+        must(Result<Unit>(must(must(pooled.matmul(hs), "head").sum(), "sum").backward()),
+             "head backward");
+        std::vector<float> dp = **must(pooled.grad(), "dP");
+        Tensor dpt = must(Tensor::create(std::move(dp), {64, 64}), "dP tensor");
+        Tensor dy = must(spread_hw(dpt, y.shape()), "spread");
+        must(Result<Unit>(y.backward_with(dy)), "stem backward");
+        must(Result<Unit>(xs.zero_grad()), "zero_grad");
+        must(Result<Unit>(ws.zero_grad()), "zero_grad");
+        must(Result<Unit>(hs.zero_grad()), "zero_grad");
+    };
+    for (int i = 0; i < 2; ++i) stem_step();
+    katsu_hip_sync(st);
+    const int stem_steps = steps > 10 ? steps / 2 : steps;
+    t0 = now();
+    for (int i = 0; i < stem_steps; ++i) stem_step();
+    katsu_hip_sync(st);
+    const double stem_ms = (now() - t0) / stem_steps * 1e3;
+    const double stem_flop = 3.0 * 2.0 * 64 * 64 * 112 * 112 * 3 * 49 + 3.0 * 2.0 * 64 * 64 * 1000;
+
     std::printf(
         "{\"conv_c3\": {\"ms_per_step\": %.4f, \"tflops\": %.3f, \"steps\": %d, "
         "\"step\": \"forward + sum + backward through Conv2D, device-resident\"}, "
         "\"matmul_1024\": {\"ms_per_step\": %.4f, \"tflops\": %.3f, \"steps\": %d, "
-        "\"step\": \"matmul + sum + backward through Tensor, device-resident\"}}\n",
+        "\"step\": \"matmul + sum + backward through Tensor, device-resident\"}, "
+        "\"stem_chain_c5\": {\"ms_per_step\": %.4f, \"tflops\": %.3f, \"steps\": %d, "
+        "\"step\": \"stem forward, mean pool, matmul head, sum, backward, spread, "
+        "stem backward; device-resident\"}}\n",
         conv_ms, conv_flop / (conv_ms * 1e-3) / 1e12, steps, mm_ms,
-        mm_flop / (mm_ms * 1e-3) / 1e12, steps);
+        mm_flop / (mm_ms * 1e-3) / 1e12, steps, stem_ms, stem_flop / (stem_ms * 1e-3) / 1e12,
+        stem_steps);
     return 0;
 }

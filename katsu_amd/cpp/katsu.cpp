@@ -453,54 +453,102 @@ struct Engine {
         if (rc != KATSU_OK) return device(rc);
         return Unit{};
     }
+
+    // tensor.rs:316-362: fresh adjoints per call; every gradient slot is
+    // checked before any is published, so a failure publishes nothing.  `seed`
+    // writes the root's adjoint into its pending buffer.
+    template <class SeedFn>
+    static Status backward_pass(const Tensor &root, const std::vector<Tensor> &order, SeedFn seed) {
+        void *st = stream();
+        Engine::Pending pending;
+        for (const Tensor &n : order) {
+            KATSU_TRY(buf, device_buffer(n.numel()));
+            pending.emplace(n.node_.get(), Engine::Slot{std::move(buf), true});
+        }
+        {
+            Engine::Slot &r = pending.at(root.node_.get());
+            const int rc = seed(r.buf.get(), st);
+            if (rc != KATSU_OK) return device(rc);
+            r.zero = false;
+        }
+        for (auto it = order.rbegin(); it != order.rend(); ++it) {
+            Engine::Slot &up = pending.at(it->node_.get());
+            if (up.zero) {  // no adjoint reached this node: its upstream is zeros
+                const int rc = katsu_hip_fill_f32_dev(up.buf.get(), it->numel(), 0.0f, st);
+                if (rc != KATSU_OK) return device(rc);
+                up.zero = false;
+            }
+            Status s = Engine::op_backward(*it, up.buf.get(), pending);
+            if (!s.ok()) return s;
+        }
+        for (const Tensor &n : order)
+            if (n.node_->borrows != 0) return err(TensorError::Kind::GradientBorrowed);
+        for (const Tensor &n : order) {
+            DeviceBuf &gradient = pending.at(n.node_.get()).buf;
+            auto &stored = n.node_->grad;
+            if (stored) {
+                const int rc =
+                    katsu_hip_accumulate_f32_dev(gradient.get(), stored->get(), n.numel(), 1.0f, st);
+                if (rc != KATSU_OK) return device(rc);
+            } else {
+                stored = std::move(gradient);
+            }
+            n.node_->grad_host_stale = true;
+        }
+        return Unit{};
+    }
 };
 
-// tensor.rs:316-362: fresh adjoints per call; every gradient slot is
-// checked before any is published, so a failure publishes nothing.
 Status Tensor::backward_with(const std::vector<float> &seed) const {
     if (seed.size() != numel()) return data_length(numel(), seed.size());
-    const std::vector<Tensor> order = topological_order();
-    void *st = stream();
-    Engine::Pending pending;
-    for (const Tensor &n : order) {
-        KATSU_TRY(buf, device_buffer(n.numel()));
-        pending.emplace(n.node_.get(), Engine::Slot{std::move(buf), true});
-    }
-    {
-        // A one-element seed (backward()) is written by a kernel, so the pass
-        // never waits on the host; longer seeds are copied in.
-        Engine::Slot &root = pending.at(node_.get());
-        const int rc = seed.size() == 1
-                           ? katsu_hip_fill_f32_dev(root.buf.get(), 1, seed[0], st)
-                           : katsu_hip_upload(root.buf.get(), seed.data(), seed.size(), st);
+    // A one-element seed (backward()) is written by a kernel, so the pass
+    // never waits on the host; longer seeds are copied in.
+    return Engine::backward_pass(*this, topological_order(), [&](float *dst, void *st) {
+        return seed.size() == 1 ? katsu_hip_fill_f32_dev(dst, 1, seed[0], st)
+                                : katsu_hip_upload(dst, seed.data(), seed.size(), st);
+    });
+}
+
+Status Tensor::backward_with(const Tensor &seed) const {
+    if (seed.numel() != numel()) return data_length(numel(), seed.numel());
+    KATSU_TRY(src, seed.device_data());
+    return Engine::backward_pass(*this, topological_order(), [&](float *dst, void *st) {
+        return katsu_hip_accumulate_f32_dev(src, dst, numel(), 0.0f, st);
+    });
+}
+
+// The config-5 head on the device (see katsu.hpp).
+Result<Tensor> mean_pool_hw(const Tensor &y) {
+    if (y.rank() != 4) return invalid_conv("input must be rank 4 (NCHW)");
+    const auto &s = y.shape();
+    KATSU_TRY(rows, element_count({s[0], s[1]}));
+    KATSU_TRY(cols, element_count({s[2], s[3]}));
+    KATSU_TRY(src, y.device_data());
+    KATSU_TRY(out, device_buffer(rows));
+    if (rows > 0) {
+        const int rc = cols == 0 ? katsu_hip_fill_f32_dev(out.get(), rows, 0.0f, stream())
+                                 : katsu_hip_mean_rows_f32_dev(src, rows, cols, out.get(),
+                                                               stream());
         if (rc != KATSU_OK) return device(rc);
-        root.zero = false;
     }
-    for (auto it = order.rbegin(); it != order.rend(); ++it) {
-        Engine::Slot &up = pending.at(it->node_.get());
-        if (up.zero) {  // no adjoint reached this node: its upstream is zeros
-            const int rc = katsu_hip_fill_f32_dev(up.buf.get(), it->numel(), 0.0f, st);
-            if (rc != KATSU_OK) return device(rc);
-            up.zero = false;
-        }
-        Status s = Engine::op_backward(*it, up.buf.get(), pending);
-        if (!s.ok()) return s;
+    return device_node(std::move(out), {s[0], s[1]}, Op{}, {}, rows);
+}
+
+Result<Tensor> spread_hw(const Tensor &dp, const std::vector<size_t> &shape) {
+    if (shape.size() != 4 || dp.rank() != 2 || dp.shape()[0] != shape[0] ||
+        dp.shape()[1] != shape[1])
+        return err(TensorError::Kind::ShapeMismatch);
+    KATSU_TRY(rows, element_count({shape[0], shape[1]}));
+    KATSU_TRY(cols, element_count({shape[2], shape[3]}));
+    KATSU_TRY(count, element_count(shape));
+    KATSU_TRY(src, dp.device_data());
+    KATSU_TRY(out, device_buffer(count));
+    if (count > 0) {
+        const int rc = katsu_hip_broadcast_rows_f32_dev(src, rows, cols, 1.0f / (float)cols,
+                                                        out.get(), 0.0f, stream());
+        if (rc != KATSU_OK) return device(rc);
     }
-    for (const Tensor &n : order)
-        if (n.node_->borrows != 0) return err(TensorError::Kind::GradientBorrowed);
-    for (const Tensor &n : order) {
-        DeviceBuf &gradient = pending.at(n.node_.get()).buf;
-        auto &stored = n.node_->grad;
-        if (stored) {
-            const int rc =
-                katsu_hip_accumulate_f32_dev(gradient.get(), stored->get(), n.numel(), 1.0f, st);
-            if (rc != KATSU_OK) return device(rc);
-        } else {
-            stored = std::move(gradient);
-        }
-        n.node_->grad_host_stale = true;
-    }
-    return Unit{};
+    return device_node(std::move(out), shape, Op{}, {}, count);
 }
 
 // ---------------------------------------------------------------------------

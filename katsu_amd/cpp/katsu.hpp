@@ -152,6 +152,9 @@ class Tensor {
 
     Status backward() const;
     Status backward_with(const std::vector<float> &seed) const;
+    // backward_with for a seed already on the device (any tensor with this
+    // tensor's element count; its values are read, its graph is not).
+    Status backward_with(const Tensor &seed) const;
 
     bool same_node(const Tensor &o) const { return node_ == o.node_; }
 
@@ -206,5 +209,13 @@ class Conv2D {
 
 // tensor.rs:127-138 (crate-internal, exposed for the tests).
 Result<size_t> element_count(const std::vector<size_t> &shape);
+
+// The stem workload's head, which katsu-core has no op
+// for, on the device: mean_pool_hw(y) is the [N, C] leaf of per-channel means
+// of an NCHW tensor; spread_hw(dp, shape) is the [N, C, H, W] leaf
+// dy[n][c][h][w] = dp[n][c] / (H*W), the pool's VJP, to seed
+// y.backward_with(dy).
+Result<Tensor> mean_pool_hw(const Tensor &y);
+Result<Tensor> spread_hw(const Tensor &dp, const std::vector<size_t> &shape);
 
 }  // namespace katsu

@@ -346,6 +346,50 @@ void empty_batch_and_seeded_initialization() {  // conv2d.rs:145-169
     for (float w : grad(layer.weights())) CHECK(w == 0.0f);
 }
 
+// ---- beyond the reference's tests: the device engine's own features -----------
+
+// The stem workload's chain on the device: pool, matmul
+// head, sum, backward into the pooled leaf, spread, and the conv backward
+// seeded with it.  The chain's gradients must equal the layer's local VJP of
+// the same seed bit for bit (same kernels, written into fresh buffers), the
+// pool must match a host mean, and dP must be the row sums of the head.
+void stem_chain_on_device() {
+    const size_t N = 2, C = 3, K = 4, J = 5;
+    V xs(N * C * 9 * 11);
+    for (size_t i = 0; i < xs.size(); ++i) xs[i] = (float)((i * 37) % 101) / 101.0f;
+    auto x = TRY(Tensor::create(xs, {N, C, 9, 11}));
+    auto layer = TRY(Conv2D::new_seeded(C, K, {3, 3}, 2, 1, 5));
+    auto y = TRY(layer.forward(x));
+    const size_t OH = y.shape()[2], OW = y.shape()[3];
+    auto p = TRY(katsu::mean_pool_hw(y));
+    CHECK(p.shape() == (std::vector<size_t>{N, K}));
+    const V &yd = y.data();
+    for (size_t r = 0; r < N * K; ++r) {
+        double acc = 0;
+        for (size_t i = 0; i < OH * OW; ++i) acc += yd[r * OH * OW + i];
+        CHECK(std::fabs(p.data()[r] - acc / (OH * OW)) <= 1e-6 * (1 + std::fabs(acc)));
+    }
+    V hs(K * J);
+    for (size_t i = 0; i < hs.size(); ++i) hs[i] = 0.25f * (float)((int)(i % 7) - 3);
+    auto h = TRY(Tensor::create(hs, {K, J}));
+    TRY(TRY(TRY(p.matmul(h)).sum()).backward());
+    const V dp = grad(p);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t k = 0; k < K; ++k) {
+            float row = 0;
+            for (size_t j = 0; j < J; ++j) row += hs[k * J + j];
+            CHECK(dp[n * K + k] == row);  // sums of quarter-integers: exact
+        }
+    auto dp_t = TRY(Tensor::create(dp, {N, K}));
+    auto dy = TRY(katsu::spread_hw(dp_t, y.shape()));
+    for (size_t i = 0; i < dy.numel(); ++i)
+        CHECK(dy.data()[i] == dp[i / (OH * OW)] * (1.0f / (float)(OH * OW)));
+    TRY(y.backward_with(dy));
+    auto [dx, dw] = TRY(layer.backward(dy));
+    CHECK(grad(x) == dx.data());
+    CHECK(grad(layer.weights()) == dw.data());
+}
+
 void known_stride_and_padding() {  // conv2d.rs:172-179
     auto x = TRY(Tensor::create(iota1(9), {1, 1, 3, 3}));
     auto layer = TRY(Conv2D::from_weights(TRY(Tensor::create({1, 2, 3, 4}, {1, 1, 2, 2})), 2, 1));
@@ -380,6 +424,7 @@ const Case kCases[] = {
     {"invalid_shapes_and_overflow", invalid_shapes_and_overflow},
     {"empty_batch_and_seeded_initialization", empty_batch_and_seeded_initialization},
     {"known_stride_and_padding", known_stride_and_padding},
+    {"stem_chain_on_device", stem_chain_on_device},
 };
 
 }  // namespace

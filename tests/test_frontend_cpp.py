@@ -39,6 +39,10 @@ DEVICE = [
     "invalid_shapes_and_overflow",
     "known_stride_and_padding",
 ]
+# The device engine's own features (no counterpart test in the reference).
+EXTRA_DEVICE = [
+    "stem_chain_on_device",
+]
 
 
 def _driver():
@@ -66,7 +70,7 @@ def host_results():
 
 @pytest.fixture(scope="module")
 def device_results():
-    return _run(DEVICE)
+    return _run(DEVICE + EXTRA_DEVICE)
 
 
 def test_every_reference_test_is_ported():
@@ -81,7 +85,7 @@ def test_frontend_host(name, host_results):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", DEVICE)
+@pytest.mark.parametrize("name", DEVICE + EXTRA_DEVICE)
 def test_frontend_device(name, device_results):
     status, line = device_results.get(name, ("MISSING", name))
     assert status == "PASS", line
