@@ -182,6 +182,16 @@ int katsu_hip_mean_rows_f32_dev(const float *y, size_t rows, size_t cols, float 
 int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, float scale,
                                      float *dy, float beta, void *stream);
 
+/* Grad-CAM over an activation map and its gradient (the raw material
+ * get_activation_map provides, conv2d.rs:140-148; the method the reference
+ * outlines in docs/conv2d.md, "O que falta para Grad-CAM"), NCHW [n][c][hw]:
+ *   alpha[n][c] = mean over hw of grad[n][c][.]
+ *   cam[n][p]   = max(0, sum_c alpha[n][c] * act[n][c][p])
+ *   then each image's map divided by its maximum (all-zero maps stay zero).
+ * cam holds n*hw floats.  No counterpart in the reference's code. */
+int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, size_t c,
+                              size_t hw, float *cam, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -156,6 +156,8 @@ std::string TensorError::to_string() const {
         case Kind::Allocation: return "tensor allocation failed";
         case Kind::Device:
             return std::string("device kernel failed: ") + katsu_hip_strerror(status);
+        case Kind::MissingGradient:
+            return "Grad-CAM requires a backward that reached the activation map";
     }
     return "unknown tensor error";
 }
@@ -703,5 +705,21 @@ std::optional<Tensor> Conv2D::get_activation_map() const {
 
 // conv2d.rs:150-153.
 void Conv2D::clear_cache() const { last_forward_->reset(); }
+
+// Grad-CAM over get_activation_map() and its gradient, on the device.
+Result<Tensor> Conv2D::grad_cam() const {
+    if (!*last_forward_) return err(TensorError::Kind::MissingForward);
+    const Tensor &map = (*last_forward_)->second;
+    const TensorNode &n = *map.node_;
+    if (!n.grad) return err(TensorError::Kind::MissingGradient);
+    const auto &s = map.shape();
+    KATSU_TRY(act, map.device_data());
+    KATSU_TRY(count, element_count({s[0], s[2], s[3]}));
+    KATSU_TRY(out, device_buffer(count));
+    const int rc = katsu_hip_gradcam_f32_dev(act, n.grad->get(), s[0], s[1], s[2] * s[3],
+                                             out.get(), stream());
+    if (rc != KATSU_OK) return device(rc);
+    return device_node(std::move(out), {s[0], s[2], s[3]}, Op{}, {}, count);
+}
 
 }  // namespace katsu

@@ -46,7 +46,8 @@ struct DeviceFault : std::runtime_error {
     explicit DeviceFault(int st);
 };
 
-// tensor.rs:9-30, plus Device for a failed library call.
+// tensor.rs:9-30, plus Device for a failed library call and MissingGradient
+// for Grad-CAM on an activation map that no backward has reached.
 struct TensorError {
     enum class Kind {
         ShapeOverflow,
@@ -60,6 +61,7 @@ struct TensorError {
         MatmulMismatch,
         Allocation,
         Device,
+        MissingGradient,
     };
     Kind kind;
     const char *message = "";  // InvalidConv
@@ -104,6 +106,7 @@ struct Op {
 };
 
 class Tensor;
+class Conv2D;
 struct TensorNode;
 
 // A shared borrow of a node's gradient (Ref<'_, Option<Vec<f32>>>): while it
@@ -168,6 +171,7 @@ class Tensor {
     Result<Tensor> elementwise(const Tensor &rhs, Op::Kind op) const;
     std::vector<Tensor> topological_order() const;
     friend struct Engine;
+    friend class Conv2D;
     std::shared_ptr<TensorNode> node_;
 };
 
@@ -196,6 +200,12 @@ class Conv2D {
     Result<std::pair<Tensor, Tensor>> backward(const Tensor &grad_output) const;  // seam S4
     std::optional<Tensor> get_activation_map() const;
     void clear_cache() const;
+    // Grad-CAM of the last forward's activation map, after a backward has
+    // given it a gradient: [N, OH, OW] maps (the method docs/conv2d.md
+    // outlines; the reference provides only the raw map): channel weights =
+    // spatial means of the gradient, ReLU of the weighted channel sum, each
+    // map divided by its maximum.  The maps are not resized to the input.
+    Result<Tensor> grad_cam() const;
 
    private:
     Conv2D(Tensor w, size_t stride, size_t padding)

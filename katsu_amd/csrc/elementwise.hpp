@@ -146,3 +146,41 @@ __global__ void __launch_bounds__(256) broadcast_rows(const float *__restrict__ 
 }
 
 }  // namespace katsu
+
+namespace katsu {
+
+// Grad-CAM, step 2: cam[n][p] = max(0, sum_c alpha[n][c] * act[n][c][p]),
+// channels summed in order; one thread per pixel.
+__global__ void __launch_bounds__(256) cam_combine(const float *__restrict__ act,
+                                                   const float *__restrict__ alpha, int64_t N,
+                                                   int64_t C, int64_t HW, float *cam) {
+    const int64_t total = N * HW;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t n = i / HW, p = i - n * HW;
+        const float *a = act + n * C * HW + p;
+        const float *al = alpha + n * C;
+        float v = 0.f;
+        for (int64_t c = 0; c < C; ++c) v += al[c] * a[c * HW];
+        cam[i] = v > 0.f ? v : 0.f;
+    }
+}
+
+// Grad-CAM, step 3: each row divided by its maximum (a row with no positive
+// value stays zero); one block per row.
+__global__ void __launch_bounds__(256) normalize_rows_by_max(float *x, int64_t cols) {
+    __shared__ float part[4];
+    float *row = x + (int64_t)blockIdx.x * cols;
+    float m = 0.f;
+    for (int64_t i = threadIdx.x; i < cols; i += 256) m = fmaxf(m, row[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_down(m, off, 64));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    if (m <= 0.f) return;
+    const float inv = 1.f / m;
+    for (int64_t i = threadIdx.x; i < cols; i += 256) row[i] *= inv;
+}
+
+}  // namespace katsu

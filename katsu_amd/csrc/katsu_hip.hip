@@ -59,6 +59,7 @@ struct State {
     Buffer staging[5];
     Buffer workspace;
     Buffer sum_scratch;  // partial sums of katsu_hip_sum_f32_dev
+    Buffer cam_scratch;  // channel weights of katsu_hip_gradcam_f32_dev
     Pool pool;
 };
 
@@ -1126,6 +1127,8 @@ void katsu_hip_shutdown(void) {
     s.workspace = Buffer{};
     if (s.sum_scratch.ptr) (void)hipFree(s.sum_scratch.ptr);
     s.sum_scratch = Buffer{};
+    if (s.cam_scratch.ptr) (void)hipFree(s.cam_scratch.ptr);
+    s.cam_scratch = Buffer{};
     for (auto &kv : s.pool.free) (void)hipFree(kv.second);
     for (auto &kv : s.pool.live) (void)hipFree(kv.first);
     s.pool = Pool{};
@@ -1454,6 +1457,27 @@ int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, f
     const int64_t n = (int64_t)rows * (int64_t)cols;
     broadcast_rows<<<ew_blocks(n), 256, 0, (hipStream_t)stream>>>(g, (int64_t)rows,
                                                                   (int64_t)cols, scale, dy, beta);
+    return launch_status();
+}
+
+int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, size_t c,
+                              size_t hw, float *cam, void *stream) {
+    if (n == 0 || hw == 0) return KATSU_OK;
+    if (!act || !grad || !cam || c == 0) return KATSU_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t N = (int64_t)n, C = (int64_t)c, HW = (int64_t)hw;
+    if (N > kI32Max) return KATSU_E_INVALID;
+    State &s = state();
+    float *alpha;
+    {
+        std::lock_guard<std::mutex> lock(s.mu);
+        int rc = ensure(s.cam_scratch, (size_t)(N * C) * sizeof(float));
+        if (rc) return rc;
+        alpha = (float *)s.cam_scratch.ptr;
+    }
+    mean_rows<<<(unsigned)cdiv(N * C, 4), 256, 0, st>>>(grad, N * C, HW, alpha);
+    cam_combine<<<ew_blocks(N * HW), 256, 0, st>>>(act, alpha, N, C, HW, cam);
+    normalize_rows_by_max<<<(unsigned)N, 256, 0, st>>>(cam, HW);
     return launch_status();
 }
 

@@ -204,3 +204,17 @@ def broadcast_rows(g, rows, cols, scale, dy=None, beta=0.0):
     check(lib().katsu_hip_broadcast_rows_f32_dev(_p(g), rows, cols, float(scale), _p(dy),
                                                   float(beta), _stream()), "broadcast_rows")
     return dy
+
+
+def grad_cam(act, grad):
+    """Grad-CAM of an NCHW activation map and its gradient: [N, H, W] maps,
+    ReLU of the channel sum weighted by the gradient's spatial means, each
+    divided by its maximum."""
+    _dev_f32(act, grad)
+    if act.shape != grad.shape or act.dim() != 4:
+        raise ValueError("activation and gradient must be the same NCHW shape")
+    n, c, h, w = act.shape
+    cam = torch.empty((n, h, w), device=act.device, dtype=torch.float32)
+    check(lib().katsu_hip_gradcam_f32_dev(_p(act), _p(grad), n, c, h * w, _p(cam), _stream()),
+          "grad_cam")
+    return cam

@@ -390,6 +390,43 @@ void stem_chain_on_device() {
     CHECK(grad(layer.weights()) == dw.data());
 }
 
+// Grad-CAM on the repository example's shapes (a seeded 3->8 layer, loss
+// sum(y*y)), against the same formula evaluated on the host from the map and
+// its downloaded gradient.
+void grad_cam_on_device() {
+    auto layer = TRY(Conv2D::new_seeded(3, 8, {3, 3}, 1, 1, 123));
+    CHECK_ERR(layer.grad_cam(), Kind::MissingForward);
+    V xs(2 * 3 * 12 * 10);
+    for (size_t i = 0; i < xs.size(); ++i) xs[i] = (float)(i % 256) / 255.0f;
+    auto x = TRY(Tensor::create(xs, {2, 3, 12, 10}));
+    auto y = TRY(layer.forward(x));
+    CHECK_ERR(layer.grad_cam(), Kind::MissingGradient);
+    TRY(TRY(TRY(y.mul(y)).sum()).backward());
+    auto cam = TRY(layer.grad_cam());
+    CHECK(cam.shape() == (std::vector<size_t>{2, 12, 10}));
+    const V &a = y.data();
+    const V g = grad(y);
+    const size_t C = 8, HW = 120;
+    for (size_t n = 0; n < 2; ++n) {
+        std::vector<double> ref(HW, 0.0);
+        double mx = 0;
+        for (size_t p = 0; p < HW; ++p) {
+            double v = 0;
+            for (size_t c = 0; c < C; ++c) {
+                double alpha = 0;
+                for (size_t q = 0; q < HW; ++q) alpha += g[(n * C + c) * HW + q];
+                v += alpha / HW * a[(n * C + c) * HW + p];
+            }
+            ref[p] = v > 0 ? v : 0;
+            mx = std::fmax(mx, ref[p]);
+        }
+        for (size_t p = 0; p < HW; ++p) {
+            const double want = mx > 0 ? ref[p] / mx : 0;
+            CHECK(std::fabs(cam.data()[n * HW + p] - want) <= 1e-5);
+        }
+    }
+}
+
 void known_stride_and_padding() {  // conv2d.rs:172-179
     auto x = TRY(Tensor::create(iota1(9), {1, 1, 3, 3}));
     auto layer = TRY(Conv2D::from_weights(TRY(Tensor::create({1, 2, 3, 4}, {1, 1, 2, 2})), 2, 1));
@@ -425,6 +462,7 @@ const Case kCases[] = {
     {"empty_batch_and_seeded_initialization", empty_batch_and_seeded_initialization},
     {"known_stride_and_padding", known_stride_and_padding},
     {"stem_chain_on_device", stem_chain_on_device},
+    {"grad_cam_on_device", grad_cam_on_device},
 };
 
 }  // namespace

@@ -42,6 +42,7 @@ DEVICE = [
 # The device engine's own features (no counterpart test in the reference).
 EXTRA_DEVICE = [
     "stem_chain_on_device",
+    "grad_cam_on_device",
 ]
 
 

@@ -93,3 +93,25 @@ def test_mean_rows_and_broadcast(dev):
     dy = ops.broadcast_rows(torch.from_numpy(g).to(dev), rows, cols, 1.0 / cols).cpu().numpy()
     assert np.array_equal(dy.reshape(rows, cols), np.repeat((g * np.float32(1.0 / cols))[:, None],
                                                             cols, 1))
+
+
+def test_grad_cam(dev):
+    """katsu_hip_gradcam_f32_dev against the formula in float64: channel
+    weights = spatial means of the gradient, ReLU of the weighted channel sum,
+    each map divided by its maximum; an all-negative map stays zero."""
+    import torch
+
+    from katsu_amd import ops
+    n, c, h, w = 3, 16, 14, 15
+    act = synth.uniform(11, (n, c, h, w))
+    grad = synth.uniform(12, (n, c, h, w))
+    act[2] = -np.abs(act[2])
+    grad[2] = np.abs(grad[2])  # image 2: every weighted sum negative
+    cam = ops.grad_cam(torch.from_numpy(act).to(dev), torch.from_numpy(grad).to(dev)).cpu().numpy()
+    a64, g64 = act.astype(np.float64), grad.astype(np.float64)
+    alpha = g64.reshape(n, c, -1).mean(2)
+    ref = np.maximum(np.einsum("nc,nchw->nhw", alpha, a64), 0.0)
+    mx = ref.reshape(n, -1).max(1)
+    ref = np.where(mx[:, None, None] > 0, ref / np.where(mx > 0, mx, 1)[:, None, None], 0.0)
+    assert np.all(cam[2] == 0.0)
+    assert np.max(np.abs(cam - ref)) <= 1e-5
