@@ -1,0 +1,247 @@
+// gemm.hpp -- the fp32 MFMA GEMM of the matmul seams (tensor.rs:264-273 and
+// the VJP, tensor.rs:424-444) for aligned problems: C = beta*C + op(A) op(B)
+// with M, N, K multiples of 4 and 16-byte aligned row-major operands.
+//
+// Block tile BM x BN with BK = 16, four waves in a 2 x 2 grid, each wave FM x
+// FN fragments of 16 x 16 (v_mfma_f32_16x16x4_f32).  Every global load and
+// LDS access is 16 bytes wide:
+//   * within a 16-deep k block, step s of lane group g (lanes 16g..16g+15)
+//     takes k = 4g + s (any bijection works if A and B agree), so an
+//     operand stored k-contiguous in LDS ([i][k]) gives one lane its four
+//     steps in one ds_read_b128;
+//   * an operand stored i-contiguous ([k][i]) is read FM floats at a time
+//     across the fragments: fragment a's MFMA row m is tile row FM*m + a;
+// and each operand keeps its global orientation in LDS, so staging never
+// transposes.  Split-K writes fixed partial slices that the caller reduces
+// in a fixed order (dw_split_reduce), so results are run-to-run identical.
+#pragma once
+
+#include "direct.hpp"
+
+namespace katsu {
+
+struct GemmArgs {
+    const float *a, *b;
+    float *c;            // C, or the partial slices when split_stride != 0
+    int M, N, K;
+    int lda, ldb, ldc;   // row strides of A, B as stored, and of the output
+    float beta;          // applied when writing C directly
+    int tiles_m, tiles_n, splits, kchunk;  // kchunk: k range of one split (multiple of 16)
+    int64_t split_stride;                  // floats between partial slices, or 0
+    uint32_t a_bytes, b_bytes;
+};
+
+template <int BM, int BN, bool TA, bool TB>
+struct GemmGeo {
+    static constexpr int BK = 16;
+    // A: TA = 0 stored [i][k] (pitch BK + 4: 16-byte rows, the 8 lanes of an
+    //    LDS cycle on distinct banks); TA = 1 stored [k][i] (pitch BM + 4).
+    static constexpr int PA = TA ? BM + 4 : BK + 4;
+    static constexpr int SA = TA ? BK * PA : BM * PA;
+    static constexpr int PB = TB ? BK + 4 : BN + 4;
+    static constexpr int SB = TB ? BN * PB : BK * PB;
+    static constexpr int STAGE = SA + SB;
+    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+};
+
+template <int N>
+struct FloatN;
+template <>
+struct FloatN<1> { using T = float; };
+template <>
+struct FloatN<2> { using T = float2; };
+template <>
+struct FloatN<4> { using T = floatx4; };
+
+template <int N>
+__device__ __forceinline__ float lane_of(const typename FloatN<N>::T &v, int i) {
+    if constexpr (N == 1) return v;
+    else if constexpr (N == 2) return i == 0 ? v.x : v.y;
+    else return v[i];
+}
+
+template <int BM, int BN, bool TA, bool TB>
+__global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
+    using Geo = GemmGeo<BM, BN, TA, TB>;
+    constexpr int BK = Geo::BK;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
+    static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
+    constexpr int A4 = BM * BK / 4 / 256;  // float4 loads per thread per tile
+    constexpr int B4 = BN * BK / 4 / 256;
+    static_assert(A4 >= 1 && B4 >= 1, "tile too small for 256 threads");
+
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wi0 = (wave >> 1) * WM, wj0 = (wave & 1) * WN;
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int split = t / (g.tiles_m * g.tiles_n);
+    const int tile = t - split * (g.tiles_m * g.tiles_n);
+    const int i0 = (tile % g.tiles_m) * BM, j0 = (tile / g.tiles_m) * BN;
+    const int kb = split * g.kchunk;
+    const int ke = min(kb + g.kchunk, g.K);
+
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, g.a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, g.b_bytes);
+    floatx4 va[A4], vb[B4];
+
+    // Global float4 of the tile at k0: A (i, k) is a[i*lda + k] (TA = 0) or
+    // a[k*lda + i] (TA = 1); B (k, j) is b[k*ldb + j] (TB = 0) or b[j*ldb + k].
+    auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < A4; ++q) {
+            const int f = q * 256 + tid;
+            int off;
+            if (!TA) {
+                const int i = f >> 2, c = f & 3;
+                const int gi = i0 + i, gk = k0 + 4 * c;
+                off = (gi < g.M && gk < ke) ? (gi * g.lda + gk) * 4 : kOOB;
+            } else {
+                const int k = f / (BM / 4), c = f % (BM / 4);
+                const int gk = k0 + k, gi = i0 + 4 * c;
+                off = (gk < ke && gi < g.M) ? (gk * g.lda + gi) * 4 : kOOB;
+            }
+            va[q] = buf_load4(ra, off);
+        }
+#pragma unroll
+        for (int q = 0; q < B4; ++q) {
+            const int f = q * 256 + tid;
+            int off;
+            if (!TB) {
+                const int k = f / (BN / 4), c = f % (BN / 4);
+                const int gk = k0 + k, gj = j0 + 4 * c;
+                off = (gk < ke && gj < g.N) ? (gk * g.ldb + gj) * 4 : kOOB;
+            } else {
+                const int j = f >> 2, c = f & 3;
+                const int gj = j0 + j, gk = k0 + 4 * c;
+                off = (gj < g.N && gk < ke) ? (gj * g.ldb + gk) * 4 : kOOB;
+            }
+            vb[q] = buf_load4(rb, off);
+        }
+    };
+    auto store = [&](float *st) __attribute__((always_inline)) {
+        float *sa = st, *sb = st + Geo::SA;
+#pragma unroll
+        for (int q = 0; q < A4; ++q) {
+            const int f = q * 256 + tid;
+            float *d = !TA ? sa + (f >> 2) * Geo::PA + 4 * (f & 3)
+                           : sa + (f / (BM / 4)) * Geo::PA + 4 * (f % (BM / 4));
+            *reinterpret_cast<floatx4 *>(d) = va[q];
+        }
+#pragma unroll
+        for (int q = 0; q < B4; ++q) {
+            const int f = q * 256 + tid;
+            float *d = !TB ? sb + (f / (BN / 4)) * Geo::PB + 4 * (f % (BN / 4))
+                           : sb + (f >> 2) * Geo::PB + 4 * (f & 3);
+            *reinterpret_cast<floatx4 *>(d) = vb[q];
+        }
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One 16-deep k block from a stage: four MFMA steps per fragment pair.
+    auto compute = [&](const float *st) __attribute__((always_inline)) {
+        const float *sa = st, *sb = st + Geo::SA;
+        floatx4 ak[FM], bk[FN];  // k-contiguous operands: four steps per read
+        if (!TA) {
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+                ak[a] = *reinterpret_cast<const floatx4 *>(sa + (wi0 + 16 * a + l16) * Geo::PA +
+                                                           4 * lg);
+        }
+        if (TB) {
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                bk[b] = *reinterpret_cast<const floatx4 *>(sb + (wj0 + 16 * b + l16) * Geo::PB +
+                                                           4 * lg);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int k = 4 * lg + s;
+            float af[FM], bf[FN];
+            if (!TA) {
+#pragma unroll
+                for (int a = 0; a < FM; ++a) af[a] = ak[a][s];
+            } else {
+                const auto v = *reinterpret_cast<const typename FloatN<FM>::T *>(
+                    sa + k * Geo::PA + wi0 + FM * l16);
+#pragma unroll
+                for (int a = 0; a < FM; ++a) af[a] = lane_of<FM>(v, a);
+            }
+            if (TB) {
+#pragma unroll
+                for (int b = 0; b < FN; ++b) bf[b] = bk[b][s];
+            } else {
+                const auto v = *reinterpret_cast<const typename FloatN<FN>::T *>(
+                    sb + k * Geo::PB + wj0 + FN * l16);
+#pragma unroll
+                for (int b = 0; b < FN; ++b) bf[b] = lane_of<FN>(v, b);
+            }
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b)
+                    acc[a][b] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+        }
+    };
+
+    if (kb < ke) {
+        float *st0 = smem, *st1 = smem + Geo::STAGE;
+        load(kb);
+        store(st0);
+        __syncthreads();
+        for (int k0 = kb; k0 < ke; k0 += 2 * BK) {
+            const bool m1 = k0 + BK < ke, m2 = k0 + 2 * BK < ke;
+            if (m1) load(k0 + BK);
+            compute(st0);
+            if (m1) store(st1);
+            __syncthreads();
+            if (!m1) break;
+            if (m2) load(k0 + 2 * BK);
+            compute(st1);
+            if (m2) store(st0);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: fragment (a, b), register v is row m = 4*lg + v, column n = l16.
+    float *out = g.split_stride ? g.c + (int64_t)split * g.split_stride : g.c;
+    const bool direct = g.split_stride == 0;
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = 4 * lg + v;
+            const int gi = i0 + wi0 + (TA ? FM * m + a : 16 * a + m);
+            if (gi >= g.M) continue;
+            float *row = out + (int64_t)gi * g.ldc;
+            if (!TB && FN == 4) {
+                const int gj = j0 + wj0 + 4 * l16;
+                if (gj < g.N) {
+                    floatx4 r = floatx4{acc[a][0][v], acc[a][1][v], acc[a][2][v], acc[a][3][v]};
+                    floatx4 *d = reinterpret_cast<floatx4 *>(row + gj);
+                    if (direct && g.beta != 0.f) r += *d;
+                    *d = r;
+                }
+            } else {
+#pragma unroll
+                for (int b = 0; b < FN; ++b) {
+                    const int gj = j0 + wj0 + (TB ? 16 * b + l16 : FN * l16 + b);
+                    if (gj < g.N) {
+                        float *p = row + gj;
+                        *p = (direct && g.beta != 0.f) ? *p + acc[a][b][v] : acc[a][b][v];
+                    }
+                }
+            }
+        }
+}
+
+}  // namespace katsu

@@ -20,6 +20,7 @@
 #include "igemm.hpp"
 #include "direct.hpp"
 #include "elementwise.hpp"
+#include "gemm.hpp"
 
 namespace katsu {
 namespace {
@@ -60,6 +61,7 @@ struct State {
     Buffer workspace;
     Buffer sum_scratch;  // partial sums of katsu_hip_sum_f32_dev
     Buffer cam_scratch;  // channel weights of katsu_hip_gradcam_f32_dev
+    Buffer gemm_ws;      // split-K partials of the GEMM
     Pool pool;
 };
 
@@ -117,6 +119,7 @@ int launch_scale(float *p, int64_t n, float beta, hipStream_t st) {
 }
 
 bool beta_ok(float beta) { return beta == 0.f || beta == 1.f; }
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // ---------------------------------------------------------------------------
 // Tile configurations.  BM spans the output's "row" dimension (oc, c, or m),
@@ -174,6 +177,92 @@ int gemm_dispatch(const float *a, const float *b, float *c, int64_t m, int64_t n
     return gemm_cfg<C, true, false>(a, 1, m, b, k, 1, c, m, n, k, beta, st);
 }
 
+int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
+                        float beta, hipStream_t st);
+State &state();
+
+template <int BM, int BN, bool TA, bool TB>
+int gemm_fast_launch(const GemmArgs &g, int64_t blocks, hipStream_t st) {
+    using Geo = GemmGeo<BM, BN, TA, TB>;
+    constexpr auto kern = gemm_kernel<BM, BN, TA, TB>;
+    kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(g);
+    return launch_status();
+}
+
+template <int BM, int BN>
+int gemm_fast_t(const GemmArgs &g, int64_t blocks, int ta, int tb, hipStream_t st) {
+    if (!ta && !tb) return gemm_fast_launch<BM, BN, false, false>(g, blocks, st);
+    if (!ta && tb) return gemm_fast_launch<BM, BN, false, true>(g, blocks, st);
+    if (ta && !tb) return gemm_fast_launch<BM, BN, true, false>(g, blocks, st);
+    return gemm_fast_launch<BM, BN, true, true>(g, blocks, st);
+}
+
+// The dedicated GEMM (gemm.hpp) for aligned problems: 128x128 tiles, or
+// 64x64 when that leaves too few blocks, and split-K up to 2 blocks per CU
+// with a fixed-order reduce of the partial slices.  False = not applicable.
+bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K, int ta,
+               int tb, float beta, hipStream_t st, int *rc) {
+    if (M % 4 || N % 4 || K % 4 || !aligned16(a) || !aligned16(b) || !aligned16(c)) return false;
+    if (M * K * 4 >= (int64_t)kMaxBufBytes || K * N * 4 >= (int64_t)kMaxBufBytes ||
+        M * N >= kI32Max)
+        return false;
+// Split-K targets about two blocks per CU, keeping at least 512 (128-tiles)
+// or 128 (64-tiles) of K per split so the k-loop hides its load latency.
+#ifndef KATSU_GEMM_TARGET
+#define KATSU_GEMM_TARGET 512
+#define KATSU_GEMM_KMIN128 512
+#define KATSU_GEMM_KMIN64 128
+#endif
+    constexpr int64_t kTarget = KATSU_GEMM_TARGET;
+    auto split_for = [&](int64_t tiles, int64_t kmin) {
+        return std::max<int64_t>(1, std::min<int64_t>(cdiv(kTarget, tiles), K / kmin));
+    };
+    int T = 128;
+    int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
+    int64_t splits = tiles >= 256 ? std::min<int64_t>(split_for(tiles, 512), 2)
+                                  : split_for(tiles, KATSU_GEMM_KMIN128);
+    if (tiles * splits < 256) {
+        T = 64;
+        tiles = cdiv(M, 64) * cdiv(N, 64);
+        splits = split_for(tiles, KATSU_GEMM_KMIN64);
+    }
+    const int64_t kchunk = (cdiv(K, splits) + 15) / 16 * 16;
+    splits = cdiv(K, kchunk);
+    GemmArgs g;
+    g.a = a;
+    g.b = b;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.lda = (int)(ta ? M : K);
+    g.ldb = (int)(tb ? K : N);
+    g.ldc = (int)N;
+    g.beta = beta;
+    g.tiles_m = (int)cdiv(M, T);
+    g.tiles_n = (int)cdiv(N, T);
+    g.splits = (int)splits;
+    g.kchunk = (int)kchunk;
+    g.a_bytes = (uint32_t)(M * K * 4);
+    g.b_bytes = (uint32_t)(K * N * 4);
+    const int64_t pstride = M * N;
+    float *ws = nullptr;
+    if (splits > 1) {
+        State &s = state();
+        std::lock_guard<std::mutex> lock(s.mu);
+        if ((*rc = ensure(s.gemm_ws, (size_t)(splits * pstride) * sizeof(float))) != KATSU_OK)
+            return true;
+        ws = (float *)s.gemm_ws.ptr;
+    }
+    g.c = splits > 1 ? ws : c;
+    g.split_stride = splits > 1 ? pstride : 0;
+    const int64_t blocks = tiles * splits;
+    *rc = T == 128 ? gemm_fast_t<128, 128>(g, blocks, ta, tb, st)
+                   : gemm_fast_t<64, 64>(g, blocks, ta, tb, st);
+    if (*rc == KATSU_OK && splits > 1)
+        *rc = launch_split_reduce(ws, c, M * N, pstride, (int)splits, beta, st);
+    return true;
+}
+
 int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_t k, int ta,
              int tb, float beta, hipStream_t st) {
     if (!beta_ok(beta) || (ta != 0 && ta != 1) || (tb != 0 && tb != 1)) return KATSU_E_INVALID;
@@ -183,8 +272,13 @@ int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_
     if (!c) return KATSU_E_INVALID;
     if (k == 0) return launch_scale(c, (int64_t)m * (int64_t)n, beta, st);
     if (!a || !b) return KATSU_E_INVALID;
-    // The largest tile that still gives every CU a block; tiny row counts
-    // take the 16-row tile.
+    {
+        int rc = KATSU_OK;
+        if (gemm_fast(a, b, c, (int64_t)m, (int64_t)n, (int64_t)k, ta, tb, beta, st, &rc))
+            return rc;
+    }
+    // The generic engine: the largest tile that still gives every CU a
+    // block; tiny row counts take the 16-row tile.
     const int64_t M = (int64_t)m, N = (int64_t)n;
     auto tiles = [&](int64_t bm, int64_t bn) { return cdiv(M, bm) * cdiv(N, bn); };
     if (m >= 128 && n >= 128 && tiles(128, 128) >= 256)
@@ -306,7 +400,6 @@ struct DirectFwdProblem {
     int64_t g_c = 0, g_r = 0, g_s = 0, g_pad = 0, g_amin = 0, g_bmin = 0, fh = 0, fw = 0;
 };
 
-bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // A planned direct forward-shaped launch: arguments, grid, weight path.
 struct DirectFwdPlan {
@@ -1129,6 +1222,8 @@ void katsu_hip_shutdown(void) {
     s.sum_scratch = Buffer{};
     if (s.cam_scratch.ptr) (void)hipFree(s.cam_scratch.ptr);
     s.cam_scratch = Buffer{};
+    if (s.gemm_ws.ptr) (void)hipFree(s.gemm_ws.ptr);
+    s.gemm_ws = Buffer{};
     for (auto &kv : s.pool.free) (void)hipFree(kv.second);
     for (auto &kv : s.pool.live) (void)hipFree(kv.first);
     s.pool = Pool{};

@@ -61,12 +61,16 @@ def test_matmul_and_vjp_parity(m, k, n, dev):
     assert_within(db.cpu().numpy(), db_ref, aa.T @ ag + np.abs(db0), m + 1, "dB")
 
 
+# (m, n, k): unaligned (the generic engine), then multiples of 4 (the
+# dedicated GEMM: 64-tiles with split-K, a long split-K reduction, 128-tiles
+# with edge tiles).
+@pytest.mark.parametrize("m,n,k", [(70, 45, 131), (72, 44, 132), (128, 96, 2048),
+                                   (516, 260, 68)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_all_transposes_beta(ta, tb, dev):
+def test_all_transposes_beta(ta, tb, m, n, k, dev):
     import torch
 
     from katsu_amd import ops
-    m, n, k = 70, 45, 131
     a = synth.uniform(7, (k, m) if ta else (m, k))
     b = synth.uniform(8, (n, k) if tb else (k, n))
     c0 = synth.uniform(9, (m, n))
