@@ -457,9 +457,11 @@ struct DirectDwArgs {
 // Compile-time part of the dW LDS layout; the G tile's pitch is chosen per
 // problem (the tightest pitch == 2 mod 4, which keeps the A reads of a
 // half-wave on 32 distinct banks).
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC>
+template <int KT, int CT, int R, int S, int ROWS, int PITCH_, int GPC>
 struct DirectDwGeo {
-    static constexpr int PITCH = 64 * CC;
+    static constexpr int PITCH = PITCH_;              // halo row pitch: 32 or a multiple of 64
+    static_assert(PITCH == 32 || PITCH % 64 == 0, "halo row pitch");
+    static_assert(PITCH != 32 || ROWS % 2 == 0, "32-float rows are staged in pairs");
     static constexpr int CPITCH = ROWS * PITCH + 2;   // == 2 (mod 32)
     static constexpr int XS = CT * CPITCH;
     static constexpr int PPITCH = CT * R * S + 4;     // partial transpose buffer
@@ -470,9 +472,11 @@ struct DirectDwGeo {
 // (16*WKF) oc x 16 c x R*S taps; each k-step reads WKF A and R*S B
 // fragments for WKF*R*S MFMAs.  FULL: every tile row is a multiple of 4
 // pixels wide, so no k-step holds a pixel past the end of its row.
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
+template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, int nb) {
-    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
+    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, PITCH, GPC>;
+    constexpr int RPL = PITCH >= 64 ? 1 : 64 / PITCH;  // halo rows per 64-lane load
+    constexpr int LPR = PITCH >= 64 ? PITCH / 64 : 1;  // 64-lane loads per halo row
     constexpr int RS = R * S;
     constexpr int WK = KT / (16 * WKF);  // waves along output channels
     constexpr int CPW = CT / 4;          // input channels staged per wave
@@ -498,14 +502,15 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
     const int te = min(tb + a.tiles_per_split, a.tiles_total);
     const int gs_floats = KT * a.gpitch;  // the G part of a stage
 
-    int colb[CC];
+    const int lrow = PITCH >= 64 ? 0 : lane / PITCH;  // the lane's row within a load
+    int colb[LPR];
 #pragma unroll
-    for (int c = 0; c < CC; ++c) {
-        const int col = c * 64 + lane;
+    for (int c = 0; c < LPR; ++c) {
+        const int col = c * 64 + (PITCH >= 64 ? lane : lane % PITCH);
         const int ix = col - a.pad;
         colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
-    float xr[CPW][ROWS][CC];
+    float xr[CPW][ROWS / RPL][LPR];
     float gr[GRW * GPC];  // scalar G path
     floatx4 gr4[GQ4];     // 16-byte G path
 
@@ -533,13 +538,13 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
         for (int j = 0; j < CPW; ++j) {
             const int ci = c0 + wave + 4 * j;
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const int iy = iy0 + r;
+            for (int r = 0; r < ROWS; r += RPL) {
+                const int iy = iy0 + r + lrow;
                 const bool rok = ci < a.C && (unsigned)iy < (unsigned)a.H;
                 const int rowb = (ci * a.H + iy) * a.W * 4;
 #pragma unroll
-                for (int c = 0; c < CC; ++c)
-                    xr[j][r][c] = buf_load(rx, rok ? rowb + colb[c] : kOOB);
+                for (int c = 0; c < LPR; ++c)
+                    xr[j][r / RPL][c] = buf_load(rx, rok ? rowb + colb[c] : kOOB);
             }
         }
         // G rows k0..k0+KT of the tile (contiguous pixels from p0).
@@ -587,14 +592,16 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                 for (int c = 0; c < GPC; ++c)
                     if (lane + c * 64 < a.gcap) gs[4 * i * a.gpitch + c * 64] = gr[i * GPC + c];
         }
+        // Lane l of a load lands at row r + l / PITCH, column l % PITCH
+        // (PITCH 32), or at column c*64 + l: offset r*PITCH + c*64 + l either way.
         float *xs = base + gs_floats + wave * Geo::CPITCH + lane;
 #pragma unroll
         for (int j = 0; j < CPW; ++j)
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
+            for (int r = 0; r < ROWS; r += RPL)
 #pragma unroll
-                for (int c = 0; c < CC; ++c)
-                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r][c];
+                for (int c = 0; c < LPR; ++c)
+                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r / RPL][c];
     };
 
     floatx4 acc[WKF][RS];
@@ -728,9 +735,9 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
     }
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
+template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a) {
-    direct_dw_block<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>(a, blockIdx.x, gridDim.x);
+    direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(a, blockIdx.x, gridDim.x);
 }
 
 // Both backward passes in one launch: blocks [0, nbx) compute dX (the
@@ -739,14 +746,14 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
 // as dX blocks retire instead of waiting for a kernel boundary.  Dynamic LDS
 // is the larger of the two needs.
 template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XPITCH, bool XWVEC, int KT,
-          int CT, int ROWS, int CC, int GPC, int WKF, bool FULL>
+          int CT, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
                                                             const DirectDwArgs dw, int nbx) {
     if ((int)blockIdx.x < nbx)
         direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC>(dx, blockIdx.x, nbx);
     else
-        direct_dw_block<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>(dw, blockIdx.x - nbx,
-                                                                gridDim.x - nbx);
+        direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(dw, blockIdx.x - nbx,
+                                                                   gridDim.x - nbx);
 }
 
 // dw[e] = beta*dw[e] + sum_s part[s][e].  Thread (e4, grp) sums splits

@@ -615,13 +615,13 @@ int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstri
     return split_reduce_g<64>(ws, dw, elems, pstride, splits, beta, st);
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, int TB>
+template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, int TB>
 bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
-    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, CC, GPC>;
-    if (d.R != R || d.S != S) return false;
+    using Geo = DirectDwGeo<KT, CT, R, S, ROWS, PITCH, GPC>;
+    if (d.R != R || d.S != S || (ST != 0 && d.st != ST)) return false;
     const int64_t tmax = Geo::GMAX;  // G tile capacity (pixels)
     const int64_t ncols = (int64_t)(d.OW - 1) * d.st + S;
-    if (ncols > 64 * CC || R > ROWS) return false;
+    if (ncols > PITCH || R > ROWS) return false;
     // Buffer resources address one image of x and of G in bytes.
     if ((int64_t)d.CHW * 4 >= (int64_t)kMaxBufBytes || (int64_t)d.KOHW * 4 >= (int64_t)kMaxBufBytes)
         return false;
@@ -701,19 +701,23 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     return true;
 }
 
-// Variant table: id, block tile (KT output x CT input channels), filter
-// R x S, halo rows and column chunks of the x tile, G tile capacity in
-// 64-pixel chunks, oc fragments per wave, and the target block count that
-// sets the split over output pixels.
+// Variant table, in order of preference: id, the stride it requires (0: any),
+// block tile (KT output x CT input channels), filter R x S, halo rows and
+// row pitch of the x tile, G tile capacity in 64-pixel chunks, oc fragments
+// per wave, and the target block count that sets the split over output
+// pixels.  Variant 1 takes stride-2 layers with small images: four output
+// rows per tile on 32-float halo rows.
 #ifndef KATSU_DW_VARIANTS
-#define KATSU_DW_VARIANTS(X) X(0, 64, 32, 3, 3, 3, 1, 1, 2, 512)
+#define KATSU_DW_VARIANTS(X)                    \
+    X(1, 2, 64, 16, 3, 3, 10, 32, 1, 1, 512)    \
+    X(0, 0, 64, 32, 3, 3, 3, 64, 1, 2, 512)
 #endif
 
 DirectDwPlan direct_dw_plan_any(const ConvDims &d) {
     DirectDwPlan pl;
-#define KATSU_DW_TRY(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)                        \
+#define KATSU_DW_TRY(id, ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB)               \
     if (pl.variant < 0 && d.K >= KT &&                                                \
-        direct_dw_plan<KT, CT, R, S, ROWS, CC, GPC, WKF, TB>(d, &pl))                 \
+        direct_dw_plan<ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB>(d, &pl))          \
         pl.variant = id;
     KATSU_DW_VARIANTS(KATSU_DW_TRY)
 #undef KATSU_DW_TRY
@@ -721,9 +725,9 @@ DirectDwPlan direct_dw_plan_any(const ConvDims &d) {
     return pl;
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL>
+template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 int dw_kernel_launch(const DirectDwPlan &pl, hipStream_t st) {
-    constexpr auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, CC, GPC, WKF, FULL>;
+    constexpr auto kern = direct_dw_kernel<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>;
     const int rc = lds_optin<kern>(kLdsMax);
     if (rc != KATSU_OK) return rc;
     kern<<<dim3((unsigned)pl.blocks), dim3(256), pl.lds_bytes, st>>>(pl.a);
@@ -748,10 +752,10 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
     dw_bind(&pl, x, gy, dw, beta, ws);
     int rc = KATSU_E_INVALID;
     switch (pl.variant) {
-#define KATSU_DW_CASE(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)                      \
-    case id:                                                                         \
-        rc = pl.full ? dw_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true>(pl, st)  \
-                     : dw_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false>(pl, st); \
+#define KATSU_DW_CASE(id, ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB)                   \
+    case id:                                                                              \
+        rc = pl.full ? dw_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true>(pl, st)   \
+                     : dw_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false>(pl, st); \
         break;
         KATSU_DW_VARIANTS(KATSU_DW_CASE)
 #undef KATSU_DW_CASE
@@ -764,12 +768,13 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
 
 // dX and dW in one launch (direct_bwd_kernel): the direct dX plan and a
 // direct dW variant with the same filter size.
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF, bool FULL,
+template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL,
           bool XWVEC>
 int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
     using XGeo = DirectFwdGeo<KATSU_FWD_VARIANT, 1>;
     constexpr auto kern = direct_bwd_kernel<FwdV::KT, FwdV::F, FwdV::CB, R, S, FwdV::ROWS,
-                                            FwdV::PITCH, XWVEC, KT, CT, ROWS, CC, GPC, WKF, FULL>;
+                                            FwdV::PITCH, XWVEC, KT, CT, ROWS, PITCH, GPC, WKF,
+                                            FULL>;
     const int rc = lds_optin<kern>(kLdsMax);
     if (rc != KATSU_OK) return rc;
     const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
@@ -778,22 +783,24 @@ int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hip
     return launch_status();
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int CC, int GPC, int WKF>
+template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
 int bwd_fused_variant(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
-    if constexpr (R == FwdV::R && S == FwdV::S) {
+    if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S) {
         if (wp.full)
-            return xp.wvec ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true, true>(xp, wp, st)
-                           : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, true, false>(xp, wp, st);
-        return xp.wvec ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false, true>(xp, wp, st)
-                       : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, CC, GPC, WKF, false, false>(xp, wp, st);
+            return xp.wvec
+                ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true, true>(xp, wp, st)
+                : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true, false>(xp, wp, st);
+        return xp.wvec
+            ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false, true>(xp, wp, st)
+            : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false, false>(xp, wp, st);
     }
     return KATSU_E_INVALID;
 }
 
 // Whether a dW variant can share a launch with the direct dX kernel.
 bool dw_variant_fusable(int variant) {
-#define KATSU_DW_FUSABLE(id, kt, ct, r, s, rows, cc, gpc, wkf, tb) \
-    if (variant == id) return r == FwdV::R && s == FwdV::S;
+#define KATSU_DW_FUSABLE(id, st, kt, ct, r, s, rows, pitch, gpc, wkf, tb) \
+    if (variant == id) return st != 2 && r == FwdV::R && s == FwdV::S;
     KATSU_DW_VARIANTS(KATSU_DW_FUSABLE)
 #undef KATSU_DW_FUSABLE
     return false;
@@ -804,8 +811,8 @@ int bwd_fused_launch(const DirectFwdPlan &xp, DirectDwPlan wp, const float *x, c
     dw_bind(&wp, x, gy, dw, beta, ws);
     int rc = KATSU_E_INVALID;
     switch (wp.variant) {
-#define KATSU_DW_FUSED(id, KT, CT, R, S, ROWS, CC, GPC, WKF, TB)              \
-    case id: rc = bwd_fused_variant<KT, CT, R, S, ROWS, CC, GPC, WKF>(xp, wp, st); break;
+#define KATSU_DW_FUSED(id, ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB)          \
+    case id: rc = bwd_fused_variant<ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st); break;
         KATSU_DW_VARIANTS(KATSU_DW_FUSED)
 #undef KATSU_DW_FUSED
         default: return KATSU_E_INVALID;
