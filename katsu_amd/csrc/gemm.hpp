@@ -2,7 +2,7 @@
 // the VJP, tensor.rs:424-444) for aligned problems: C = beta*C + op(A) op(B)
 // with M, N, K multiples of 4 and 16-byte aligned row-major operands.
 //
-// Block tile BM x BN with BK = 16, four waves in a 2 x 2 grid, each wave FM x
+// Block tile BM x BN x BK (BK a multiple of 16), four waves in a 2 x 2 grid, each wave FM x
 // FN fragments of 16 x 16 (v_mfma_f32_16x16x4_f32).  Every global load and
 // LDS access is 16 bytes wide:
 //   * within a 16-deep k block, step s of lane group g (lanes 16g..16g+15)
@@ -31,9 +31,10 @@ struct GemmArgs {
     uint32_t a_bytes, b_bytes;
 };
 
-template <int BM, int BN, bool TA, bool TB>
+template <int BM, int BN, int BK_, bool TA, bool TB>
 struct GemmGeo {
-    static constexpr int BK = 16;
+    static constexpr int BK = BK_;
+    static_assert(BK % 16 == 0, "whole 16-deep k blocks");
     // A: TA = 0 stored [i][k] (pitch BK + 4: 16-byte rows, the 8 lanes of an
     //    LDS cycle on distinct banks); TA = 1 stored [k][i] (pitch BM + 4).
     static constexpr int PA = TA ? BM + 4 : BK + 4;
@@ -60,9 +61,9 @@ __device__ __forceinline__ float lane_of(const typename FloatN<N>::T &v, int i) 
     else return v[i];
 }
 
-template <int BM, int BN, bool TA, bool TB>
+template <int BM, int BN, int BK_, bool TA, bool TB>
 __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
-    using Geo = GemmGeo<BM, BN, TA, TB>;
+    using Geo = GemmGeo<BM, BN, BK_, TA, TB>;
     constexpr int BK = Geo::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 16, FN = WN / 16;
@@ -96,7 +97,7 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
             const int f = q * 256 + tid;
             int off;
             if (!TA) {
-                const int i = f >> 2, c = f & 3;
+                const int i = f / (BK / 4), c = f % (BK / 4);
                 const int gi = i0 + i, gk = k0 + 4 * c;
                 off = (gi < g.M && gk < ke) ? (gi * g.lda + gk) * 4 : kOOB;
             } else {
@@ -115,7 +116,7 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
                 const int gk = k0 + k, gj = j0 + 4 * c;
                 off = (gk < ke && gj < g.N) ? (gk * g.ldb + gj) * 4 : kOOB;
             } else {
-                const int j = f >> 2, c = f & 3;
+                const int j = f / (BK / 4), c = f % (BK / 4);
                 const int gj = j0 + j, gk = k0 + 4 * c;
                 off = (gj < g.N && gk < ke) ? (gj * g.ldb + gk) * 4 : kOOB;
             }
@@ -127,7 +128,7 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < A4; ++q) {
             const int f = q * 256 + tid;
-            float *d = !TA ? sa + (f >> 2) * Geo::PA + 4 * (f & 3)
+            float *d = !TA ? sa + (f / (BK / 4)) * Geo::PA + 4 * (f % (BK / 4))
                            : sa + (f / (BM / 4)) * Geo::PA + 4 * (f % (BM / 4));
             *reinterpret_cast<floatx4 *>(d) = va[q];
         }
@@ -135,7 +136,7 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
         for (int q = 0; q < B4; ++q) {
             const int f = q * 256 + tid;
             float *d = !TB ? sb + (f / (BN / 4)) * Geo::PB + 4 * (f % (BN / 4))
-                           : sb + (f >> 2) * Geo::PB + 4 * (f & 3);
+                           : sb + (f / (BK / 4)) * Geo::PB + 4 * (f % (BK / 4));
             *reinterpret_cast<floatx4 *>(d) = vb[q];
         }
     };
@@ -146,50 +147,54 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
 #pragma unroll
         for (int b = 0; b < FN; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // One 16-deep k block from a stage: four MFMA steps per fragment pair.
+    // The BK-deep tile of a stage: BK/16 blocks of four MFMA steps per
+    // fragment pair.
     auto compute = [&](const float *st) __attribute__((always_inline)) {
         const float *sa = st, *sb = st + Geo::SA;
-        floatx4 ak[FM], bk[FN];  // k-contiguous operands: four steps per read
-        if (!TA) {
 #pragma unroll
-            for (int a = 0; a < FM; ++a)
-                ak[a] = *reinterpret_cast<const floatx4 *>(sa + (wi0 + 16 * a + l16) * Geo::PA +
-                                                           4 * lg);
-        }
-        if (TB) {
-#pragma unroll
-            for (int b = 0; b < FN; ++b)
-                bk[b] = *reinterpret_cast<const floatx4 *>(sb + (wj0 + 16 * b + l16) * Geo::PB +
-                                                           4 * lg);
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int k = 4 * lg + s;
-            float af[FM], bf[FN];
+        for (int kq = 0; kq < BK / 16; ++kq) {
+            floatx4 ak[FM], bk[FN];  // k-contiguous operands: four steps per read
             if (!TA) {
 #pragma unroll
-                for (int a = 0; a < FM; ++a) af[a] = ak[a][s];
-            } else {
-                const auto v = *reinterpret_cast<const typename FloatN<FM>::T *>(
-                    sa + k * Geo::PA + wi0 + FM * l16);
-#pragma unroll
-                for (int a = 0; a < FM; ++a) af[a] = lane_of<FM>(v, a);
+                for (int a = 0; a < FM; ++a)
+                    ak[a] = *reinterpret_cast<const floatx4 *>(
+                        sa + (wi0 + 16 * a + l16) * Geo::PA + 16 * kq + 4 * lg);
             }
             if (TB) {
 #pragma unroll
-                for (int b = 0; b < FN; ++b) bf[b] = bk[b][s];
-            } else {
-                const auto v = *reinterpret_cast<const typename FloatN<FN>::T *>(
-                    sb + k * Geo::PB + wj0 + FN * l16);
-#pragma unroll
-                for (int b = 0; b < FN; ++b) bf[b] = lane_of<FN>(v, b);
+                for (int b = 0; b < FN; ++b)
+                    bk[b] = *reinterpret_cast<const floatx4 *>(
+                        sb + (wj0 + 16 * b + l16) * Geo::PB + 16 * kq + 4 * lg);
             }
 #pragma unroll
-            for (int a = 0; a < FM; ++a)
+            for (int s = 0; s < 4; ++s) {
+                const int k = 16 * kq + 4 * lg + s;
+                float af[FM], bf[FN];
+                if (!TA) {
 #pragma unroll
-                for (int b = 0; b < FN; ++b)
-                    acc[a][b] =
-                        __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+                    for (int a = 0; a < FM; ++a) af[a] = ak[a][s];
+                } else {
+                    const auto v = *reinterpret_cast<const typename FloatN<FM>::T *>(
+                        sa + k * Geo::PA + wi0 + FM * l16);
+#pragma unroll
+                    for (int a = 0; a < FM; ++a) af[a] = lane_of<FM>(v, a);
+                }
+                if (TB) {
+#pragma unroll
+                    for (int b = 0; b < FN; ++b) bf[b] = bk[b][s];
+                } else {
+                    const auto v = *reinterpret_cast<const typename FloatN<FN>::T *>(
+                        sb + k * Geo::PB + wj0 + FN * l16);
+#pragma unroll
+                    for (int b = 0; b < FN; ++b) bf[b] = lane_of<FN>(v, b);
+                }
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int b = 0; b < FN; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b],
+                                                                         0, 0, 0);
+            }
         }
     };
 

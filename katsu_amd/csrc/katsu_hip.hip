@@ -181,52 +181,60 @@ int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstri
                         float beta, hipStream_t st);
 State &state();
 
-template <int BM, int BN, bool TA, bool TB>
+template <int BM, int BN, int BK, bool TA, bool TB>
 int gemm_fast_launch(const GemmArgs &g, int64_t blocks, hipStream_t st) {
-    using Geo = GemmGeo<BM, BN, TA, TB>;
-    constexpr auto kern = gemm_kernel<BM, BN, TA, TB>;
+    using Geo = GemmGeo<BM, BN, BK, TA, TB>;
+    constexpr auto kern = gemm_kernel<BM, BN, BK, TA, TB>;
     kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(g);
     return launch_status();
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 int gemm_fast_t(const GemmArgs &g, int64_t blocks, int ta, int tb, hipStream_t st) {
-    if (!ta && !tb) return gemm_fast_launch<BM, BN, false, false>(g, blocks, st);
-    if (!ta && tb) return gemm_fast_launch<BM, BN, false, true>(g, blocks, st);
-    if (ta && !tb) return gemm_fast_launch<BM, BN, true, false>(g, blocks, st);
-    return gemm_fast_launch<BM, BN, true, true>(g, blocks, st);
+    if (!ta && !tb) return gemm_fast_launch<BM, BN, BK, false, false>(g, blocks, st);
+    if (!ta && tb) return gemm_fast_launch<BM, BN, BK, false, true>(g, blocks, st);
+    if (ta && !tb) return gemm_fast_launch<BM, BN, BK, true, false>(g, blocks, st);
+    return gemm_fast_launch<BM, BN, BK, true, true>(g, blocks, st);
 }
 
-// The dedicated GEMM (gemm.hpp) for aligned problems: 128x128 tiles, or
-// 64x64 when that leaves too few blocks, and split-K up to 2 blocks per CU
-// with a fixed-order reduce of the partial slices.  False = not applicable.
+// Tile choice: the largest square tile (128, 64, 32) that gives every CU a
+// block without splitting K; otherwise 64-tiles with split-K up to about
+// one block per CU, at least 128 of K per split so the k-loop hides its load
+// latency.  A split adds a reduce kernel, so it is the last resort.
+#ifndef KATSU_GEMM_TARGET
+#define KATSU_GEMM_TARGET 256
+#define KATSU_GEMM_KMIN64 128
+#endif
+#ifndef KATSU_GEMM_BK64
+#define KATSU_GEMM_BK64 64
+#endif
+
+// The dedicated GEMM (gemm.hpp) for aligned problems, with a fixed-order
+// reduce of the partial slices when K is split.  False = not applicable.
 bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K, int ta,
                int tb, float beta, hipStream_t st, int *rc) {
     if (M % 4 || N % 4 || K % 4 || !aligned16(a) || !aligned16(b) || !aligned16(c)) return false;
     if (M * K * 4 >= (int64_t)kMaxBufBytes || K * N * 4 >= (int64_t)kMaxBufBytes ||
         M * N >= kI32Max)
         return false;
-// Split-K targets about two blocks per CU, keeping at least 512 (128-tiles)
-// or 128 (64-tiles) of K per split so the k-loop hides its load latency.
-#ifndef KATSU_GEMM_TARGET
-#define KATSU_GEMM_TARGET 512
-#define KATSU_GEMM_KMIN128 512
-#define KATSU_GEMM_KMIN64 128
-#endif
-    constexpr int64_t kTarget = KATSU_GEMM_TARGET;
-    auto split_for = [&](int64_t tiles, int64_t kmin) {
-        return std::max<int64_t>(1, std::min<int64_t>(cdiv(kTarget, tiles), K / kmin));
-    };
-    int T = 128;
-    int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
-    int64_t splits = tiles >= 256 ? std::min<int64_t>(split_for(tiles, 512), 2)
-                                  : split_for(tiles, KATSU_GEMM_KMIN128);
-    if (tiles * splits < 256) {
-        T = 64;
-        tiles = cdiv(M, 64) * cdiv(N, 64);
-        splits = split_for(tiles, KATSU_GEMM_KMIN64);
+    auto tiles_of = [&](int64_t t) { return cdiv(M, t) * cdiv(N, t); };
+    int T = 0;
+    int64_t tiles = 0, splits = 1;
+    for (int t : {128, 64, 32}) {
+        if (tiles_of(t) >= 256) {
+            T = t;
+            tiles = tiles_of(t);
+            break;
+        }
     }
-    const int64_t kchunk = (cdiv(K, splits) + 15) / 16 * 16;
+    if (T == 0) {
+        T = 64;
+        tiles = tiles_of(64);
+        splits = std::max<int64_t>(
+            1, std::min<int64_t>(cdiv(KATSU_GEMM_TARGET, tiles), K / KATSU_GEMM_KMIN64));
+    }
+    const int64_t kq = T == 128 ? 16 : T == 64 ? KATSU_GEMM_BK64 : 32;  // the tile's k depth
+    const int64_t kchunk = (cdiv(K, splits) + kq - 1) / kq * kq;
     splits = cdiv(K, kchunk);
     GemmArgs g;
     g.a = a;
@@ -256,8 +264,9 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     g.c = splits > 1 ? ws : c;
     g.split_stride = splits > 1 ? pstride : 0;
     const int64_t blocks = tiles * splits;
-    *rc = T == 128 ? gemm_fast_t<128, 128>(g, blocks, ta, tb, st)
-                   : gemm_fast_t<64, 64>(g, blocks, ta, tb, st);
+    *rc = T == 128  ? gemm_fast_t<128, 128, 16>(g, blocks, ta, tb, st)
+          : T == 64 ? gemm_fast_t<64, 64, KATSU_GEMM_BK64>(g, blocks, ta, tb, st)
+                    : gemm_fast_t<32, 32, 32>(g, blocks, ta, tb, st);
     if (*rc == KATSU_OK && splits > 1)
         *rc = launch_split_reduce(ws, c, M * N, pstride, (int)splits, beta, st);
     return true;
