@@ -740,20 +740,21 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
     direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(a, blockIdx.x, gridDim.x);
 }
 
-// Both backward passes in one launch: blocks [0, nbx) compute dX (the
-// forward kernel on G with the transposed, flipped filter), the rest the dW
-// partials.  The dX blocks are dispatched first, so dW blocks fill the CUs
-// as dX blocks retire instead of waiting for a kernel boundary.  Dynamic LDS
-// is the larger of the two needs.
+// Both backward passes in one launch: blocks [0, nbw) compute the dW
+// partials, the rest dX (the forward kernel on G with the transposed,
+// flipped filter).  The dW blocks are the longer ones and are dispatched
+// first; dX blocks fill the CUs beside them and as they retire, so the two
+// passes share one ramp and one tail.  Dynamic LDS is the larger of the two
+// needs.
 template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XPITCH, bool XWVEC, int KT,
           int CT, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
-                                                            const DirectDwArgs dw, int nbx) {
-    if ((int)blockIdx.x < nbx)
-        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC>(dx, blockIdx.x, nbx);
+                                                            const DirectDwArgs dw, int nbw) {
+    if ((int)blockIdx.x < nbw)
+        direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(dw, blockIdx.x, nbw);
     else
-        direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(dw, blockIdx.x - nbx,
-                                                                   gridDim.x - nbx);
+        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC>(
+            dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
 // dw[e] = beta*dw[e] + sum_s part[s][e].  Thread (e4, grp) sums splits

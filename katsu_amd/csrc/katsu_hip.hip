@@ -624,8 +624,8 @@ int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstri
     return split_reduce_g<64>(ws, dw, elems, pstride, splits, beta, st);
 }
 
-template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, int TB>
-bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
+template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
+bool direct_dw_plan(const ConvDims &d, int64_t target_blocks, DirectDwPlan *pl) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, PITCH, GPC>;
     if (d.R != R || d.S != S || (ST != 0 && d.st != ST)) return false;
     const int64_t tmax = Geo::GMAX;  // G tile capacity (pixels)
@@ -653,7 +653,7 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     const int64_t tiles_img = cdiv(d.OH, trows) * segs;
     const int64_t tiles_total = (int64_t)d.N * tiles_img;
     const int64_t kb = cdiv(d.K, KT), cb = cdiv(d.C, CT);
-    int64_t splits = std::max<int64_t>(1, cdiv(TB, kb * cb));
+    int64_t splits = std::max<int64_t>(1, cdiv(target_blocks, kb * cb));
     splits = std::min(splits, tiles_total);
     const int64_t tps = cdiv(tiles_total, splits);
     splits = cdiv(tiles_total, tps);
@@ -722,11 +722,13 @@ bool direct_dw_plan(const ConvDims &d, DirectDwPlan *pl) {
     X(0, 0, 64, 32, 3, 3, 3, 64, 1, 2, 512)
 #endif
 
-DirectDwPlan direct_dw_plan_any(const ConvDims &d) {
+// The first variant that plans (only `variant` when it is given), with its
+// target block count divided by `tb_div`.
+DirectDwPlan direct_dw_plan_any(const ConvDims &d, int variant = -1, int tb_div = 1) {
     DirectDwPlan pl;
-#define KATSU_DW_TRY(id, ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB)               \
-    if (pl.variant < 0 && d.K >= KT &&                                                \
-        direct_dw_plan<ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB>(d, &pl))          \
+#define KATSU_DW_TRY(id, ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF, TB)                      \
+    if (pl.variant < 0 && (variant < 0 || variant == id) && d.K >= KT &&                     \
+        direct_dw_plan<ST, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(d, TB / tb_div, &pl))        \
         pl.variant = id;
     KATSU_DW_VARIANTS(KATSU_DW_TRY)
 #undef KATSU_DW_TRY
@@ -788,7 +790,7 @@ int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hip
     if (rc != KATSU_OK) return rc;
     const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
     kern<<<dim3((unsigned)(xp.blocks + wp.blocks)), dim3(256), lds, st>>>(xp.a, wp.a,
-                                                                         (int)xp.blocks);
+                                                                         (int)wp.blocks);
     return launch_status();
 }
 
@@ -1080,6 +1082,10 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 
+#ifndef KATSU_FUSED_DW_TBDIV
+#define KATSU_FUSED_DW_TBDIV 2
+#endif
+
 // Both backward passes (backward_buffers, conv2d.rs:265-292).  When dX and
 // dW both take their direct kernels they run as one launch; otherwise dX then
 // dW, as two.
@@ -1104,18 +1110,25 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
         if (rc != KATSU_OK) return rc;
         return conv_bwd_filter_dev(x, gy, dw, g, beta, ws, ws_bytes, st, fallback);
     }
+    // The shared launch takes the dW split with half the blocks: each dW
+    // block then lasts about as long as two dX blocks, the dW blocks go
+    // first, and half as many partials are written and summed.  The
+    // workspace it needs is at most the standalone plan's, which the
+    // workspace query reports.
+    DirectDwPlan wp = direct_dw_plan_any(d, wpl.direct.variant, KATSU_FUSED_DW_TBDIV);
+    if (!wp.ok || wp.ws_bytes > wpl.ws_bytes) wp = wpl.direct;
     float *wsp = (float *)ws;
-    if (wpl.ws_bytes > 0) {
+    if (wp.ws_bytes > 0) {
         if (!wsp) {
             if (!fallback) return KATSU_E_INVALID;
-            const int rc = ensure(*fallback, wpl.ws_bytes);
+            const int rc = ensure(*fallback, wp.ws_bytes);
             if (rc != KATSU_OK) return rc;
             wsp = (float *)fallback->ptr;
         } else if (ws_bytes < wpl.ws_bytes) {
             return KATSU_E_INVALID;
         }
     }
-    return bwd_fused_launch(xp, wpl.direct, x, gy, dw, beta, wsp, st);
+    return bwd_fused_launch(xp, wp, x, gy, dw, beta, wsp, st);
 }
 
 // ---------------------------------------------------------------------------

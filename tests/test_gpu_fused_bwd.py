@@ -1,26 +1,29 @@
 """The one-call backward (katsu_hip_conv2d_bwd_f32[_dev]) against the two
-separate passes.  Where dX and dW share one launch the kernels and their
-summation order are those of the separate launches, so the results must be
-identical bit for bit; shapes the fused launch does not take (stride 2,
-small channel counts, other filter sizes) go through the separate passes and
-must match them too.  beta = 1 accumulates into both outputs."""
+separate passes.  Where dX and dW share one launch, dX comes from the same
+kernel and summation order as the separate call and must be identical bit for
+bit; dW splits its pixel reduction into half as many partials there, so it
+must agree with the separate call within the bound of two fp32 sums of the
+same products.  Shapes the fused launch does not take (stride 2, small channel
+counts, other filter sizes) go through the separate passes and must match
+them bit for bit.  beta = 1 accumulates into both outputs."""
 import numpy as np
 import pytest
 
 from katsu_amd import synth
 from oracle import oracle as O
-from tests.parity import assert_within
+from tests.parity import assert_within, gamma
 
 pytestmark = pytest.mark.gpu
 
+# (x shape, w shape, stride, pad, whether dX and dW share one launch)
 CASES = [
-    ((32, 64, 56, 56), (64, 64, 3, 3), 1, 1),   # config 3: fused launch
-    ((32, 64, 30, 30), (64, 64, 3, 3), 1, 1),   # fused, rows not a multiple of 4 (masked dW)
-    ((32, 80, 28, 28), (96, 80, 3, 3), 1, 1),   # fused, channel counts off the tiles
-    ((2, 80, 17, 9), (96, 80, 3, 3), 1, 0),     # too few blocks to fuse: separate passes
-    ((4, 128, 28, 28), (256, 128, 3, 3), 2, 1),  # stride 2: separate passes
-    ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3),      # stem-like: separate passes
-    ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0),     # 1x1: separate passes
+    ((32, 64, 56, 56), (64, 64, 3, 3), 1, 1, True),    # config 3
+    ((32, 64, 30, 30), (64, 64, 3, 3), 1, 1, True),    # rows not a multiple of 4 (masked dW)
+    ((32, 80, 28, 28), (96, 80, 3, 3), 1, 1, True),    # channel counts off the tiles
+    ((2, 80, 17, 9), (96, 80, 3, 3), 1, 0, False),     # too few blocks to fuse
+    ((4, 128, 28, 28), (256, 128, 3, 3), 2, 1, False),  # stride 2
+    ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3, False),      # stem-like
+    ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0, False),     # 1x1
 ]
 
 
@@ -33,12 +36,20 @@ def _tensors(xs, ws, st, p, dev):
     return [torch.from_numpy(a).to(dev) for a in (x, w, g)]
 
 
-@pytest.mark.parametrize("xs,ws,st,p", CASES)
-def test_fused_matches_separate(xs, ws, st, p, dev):
+@pytest.mark.parametrize("xs,ws,st,p,fused", CASES)
+def test_fused_matches_separate(xs, ws, st, p, fused, dev):
     import torch
 
     from katsu_amd import ops
     x, w, g = _tensors(xs, ws, st, p, dev)
+    # Both dW sums lie within 2*gamma(K)*S of the exact one, S the same sum
+    # over |x|*|G| (computed here in fp32, hence the 1e-5 margin), so they lie
+    # within twice that of each other; with beta = 1 each result adds one more
+    # rounding of its own magnitude.
+    oshape = synth.out_shape({"x": xs, "w": ws, "stride": st, "pad": p})
+    kred = xs[0] * oshape[2] * oshape[3]
+    s_abs = ops.conv2d_backward_filter(x.abs(), g.abs(), w.shape, st, p).double()
+    lim = 4.0 * gamma(kred) * s_abs * (1 + 1e-5)
     for beta in (0.0, 1.0):
         dx0 = torch.randn(x.shape, device=dev) if beta else None
         dw0 = torch.randn(w.shape, device=dev) if beta else None
@@ -51,7 +62,13 @@ def test_fused_matches_separate(xs, ws, st, p, dev):
                                          dw=None if dw0 is None else dw0.clone(), beta=beta)
         torch.cuda.synchronize()
         assert torch.equal(dx_f, dx_s), f"dX beta={beta}"
-        assert torch.equal(dw_f, dw_s), f"dW beta={beta}"
+        if not fused:
+            assert torch.equal(dw_f, dw_s), f"dW beta={beta}"
+            continue
+        err = (dw_f.double() - dw_s.double()).abs()
+        lim_b = lim + 2.0 ** -24 * (dw_f.double().abs() + dw_s.double().abs())
+        assert bool((err <= lim_b).all()), \
+            f"dW beta={beta}: worst excess {(err - lim_b).max().item():.3e}"
 
 
 def test_fused_caller_workspace_and_graph_replay(dev):
@@ -81,9 +98,11 @@ def test_fused_caller_workspace_and_graph_replay(dev):
 
 def test_fused_host_entry_against_oracle():
     """The host-pointer form (what katsu-core's backward_buffers would call)
-    against the CPU oracle."""
+    against the CPU oracle, at a size that takes the shared launch (256 dX
+    blocks; 384 dW row tiles, 128 partials there against 192 in the separate
+    dW call)."""
     from katsu_amd import host
-    xs, ws, st, p = (2, 64, 14, 14), (64, 64, 3, 3), 1, 1
+    xs, ws, st, p = (16, 64, 24, 24), (64, 64, 3, 3), 1, 1
     c = {"x": xs, "w": ws, "stride": st, "pad": p}
     x = synth.uniform(synth.SEED_X, xs, -1.0, 1.0)
     w = synth.normal(synth.SEED_W, ws)
@@ -92,4 +111,4 @@ def test_fused_host_entry_against_oracle():
     dx_ref, dw_ref = O.conv2d_backward(x, w, g, st, p)
     dxs, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
     assert_within(dx, dx_ref, dxs, 64 * 9, "fused host dX")
-    assert_within(dw, dw_ref, dws, 2 * 14 * 14, "fused host dW")
+    assert_within(dw, dw_ref, dws, 16 * 24 * 24, "fused host dW")
