@@ -11,7 +11,10 @@ Prints ONE JSON line.  The steps, each pass and the matmul steps are captured
 as HIP graphs on torch's capture stream (the C ABI launches on the stream it
 is given) and replayed between HIP events, so the timings are GPU time, not
 Python launch overhead; the step's replays are checked against the eager
-result.
+result.  Each pass reports its mean, median and interquartile range over the
+replays, its TFLOP/s and its algorithmic GB/s.  With the CPU leg on, the CPU
+oracle's outputs and the GPU's are both compared with exact f64 dot products
+on 4096 sampled elements of y, dX and dW ("accuracy").
 """
 import argparse
 import json
@@ -59,9 +62,10 @@ def capture(fn):
 def timed_steps(step, k):
     """Captures `step` STEPS_PER_GRAPH times over in one HIP graph (and the
     remainder of k in a second) and returns the milliseconds that replaying
-    exactly k steps takes.  Several steps per graph keep the per-replay launch
-    cost of a HIP graph out of the per-step time, as a training loop captured
-    whole would."""
+    exactly k steps takes, and the per-step milliseconds of each full replay
+    (events between replays).  Several steps per graph keep the per-replay
+    launch cost of a HIP graph out of the per-step time, as a training loop
+    captured whole would."""
     import torch
     per = max(1, min(STEPS_PER_GRAPH, k))
     full, rem = divmod(k, per)
@@ -69,16 +73,27 @@ def timed_steps(step, k):
     g_rem = capture(lambda: [step() for _ in range(rem)]) if rem else None
     g_full.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(full + 1)]
     end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(full):
+    marks[0].record()
+    for i in range(full):
         g_full.replay()
+        marks[i + 1].record()
     if g_rem is not None:
         g_rem.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end)
+    spread = [marks[i].elapsed_time(marks[i + 1]) / per for i in range(full)]
+    return marks[0].elapsed_time(end), spread
+
+
+def med_iqr(vals):
+    """Median and interquartile range (linear interpolation)."""
+    import numpy as np
+    if not vals:
+        return None, None
+    q1, med, q3 = np.percentile(np.asarray(vals, np.float64), [25, 50, 75])
+    return float(med), float(q3 - q1)
 
 
 def cpu_model():
@@ -92,11 +107,12 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(cfg, images, flops_per_image):
+def cpu_baseline(cfg, images, flops_per_image, outputs=None):
     """The oracle (C restatement of the reference loops, single thread) on a
     bounded sample of the same workload: `images` of the batch, one forward
     plus one backward_buffers pass (dX and dW in one visit, as the reference
-    computes them)."""
+    computes them).  With the whole batch, the oracle's outputs are kept in
+    `outputs` for the accuracy report."""
     import numpy as np
 
     from katsu_amd import synth
@@ -106,9 +122,11 @@ def cpu_baseline(cfg, images, flops_per_image):
     x, w = synth.conv_inputs(c)
     g = np.ones(synth.out_shape(c), np.float32)
     t0 = time.perf_counter()
-    O.conv2d_forward(x, w, c["stride"], c["pad"])
-    O.conv2d_backward(x, w, g, c["stride"], c["pad"])
+    y = O.conv2d_forward(x, w, c["stride"], c["pad"])
+    dx, dw = O.conv2d_backward(x, w, g, c["stride"], c["pad"])
     dt = time.perf_counter() - t0
+    if outputs is not None and images == cfg["x"][0]:
+        outputs.update(x=x, w=w, g=g, y=y, dx=dx, dw=dw)
     return {
         "value": round(flops_per_image * images / dt / 1e12, 6),
         "unit": "TFLOP/s",
@@ -118,6 +136,48 @@ def cpu_baseline(cfg, images, flops_per_image):
                    f"(dX and dW in one visit pass), {dt:.2f} s on 1 thread of "
                    f"{cpu_model()} ({os.cpu_count()} logical CPUs visible)"),
     }
+
+
+def accuracy_report(cpu, gpu, st, pad, count=4096):
+    """GPU-vs-f64 and CPU-vs-f64 errors on `count` sampled elements of y, dX
+    and dW (exact f64 dot products), as |v - exact| / S with S = sum |a||b|:
+    the dot-product bound is 2*gamma(K_red) in these units.  Also the
+    reference's mixed metric (tests/conv2d.rs:5-13) between the GPU and CPU
+    outputs over every element."""
+    import numpy as np
+
+    from tests.parity import gamma, max_rel_mixed, sample_dw, sample_dx, sample_fwd
+    x, w, g = cpu["x"], cpu["w"], cpu["g"]
+    rng = np.random.default_rng(7)
+
+    def pick(shape):
+        size = int(np.prod(shape))
+        flat = rng.choice(size, min(count, size), replace=False)
+        return [tuple(int(i) for i in idx) for idx in zip(*np.unravel_index(flat, shape))]
+
+    n, c, h, wd = x.shape
+    k, _, r, s_ = w.shape
+    oh, ow = g.shape[2], g.shape[3]
+    kred = {"y": c * r * s_, "dx": k * r * s_ // (st * st) or 1, "dw": n * oh * ow}
+    out = {"samples": {}, "gpu_vs_f64": {}, "cpu_vs_f64": {}, "bound_2gamma": {},
+           "mixed_gpu_vs_cpu": {},
+           "units": "max over samples of |v - exact f64| / sum|a||b|"}
+    for name, samp in (("y", lambda ix: sample_fwd(x, w, st, pad, ix)),
+                       ("dx", lambda ix: sample_dx(g, w, x.shape, st, pad, ix)),
+                       ("dw", lambda ix: sample_dw(x, g, w.shape, st, pad, ix))):
+        idx = pick(cpu[name].shape)
+        exact, sabs = samp(idx)
+        sel = tuple(np.array(idx).T)
+        for side, arr in (("gpu_vs_f64", gpu[name]), ("cpu_vs_f64", cpu[name])):
+            v = arr[sel].astype(np.float64)
+            err = np.abs(v - exact)
+            rel = np.where(sabs > 0, err / np.where(sabs > 0, sabs, 1.0),
+                           np.where(err == 0, 0.0, np.inf))
+            out[side][name] = float(f"{rel.max():.3e}")
+        out["samples"][name] = len(idx)
+        out["bound_2gamma"][name] = float(f"{2 * gamma(kred[name]):.3e}")
+        out["mixed_gpu_vs_cpu"][name] = float(f"{max_rel_mixed(gpu[name], cpu[name]):.3e}")
+    return out
 
 
 def main():
@@ -196,9 +256,16 @@ def main():
     g_pass = {name: capture(lambda fn=fn: [fn() for _ in range(PASS_REPS)])
               for name, fn, _ in passes}
     pass_units = {name: units for name, _, units in passes}
+    # Algorithmic bytes of each pass: every operand read once, every output
+    # written once (f32).
+    nx, nw, ny = x.size * 4, w.size * 4, int(np.prod(yshape)) * 4
+    pass_bytes = {"fwd": nx + nw + ny, "bwd": nx + nw + ny + nx + nw,
+                  "bwd_data": ny + nw + nx, "bwd_filter": nx + ny + nw}
 
     torch.cuda.synchronize()
-    ms_per_step = timed_steps(step, args.steps) / args.steps
+    total_ms, spread = timed_steps(step, args.steps)
+    ms_per_step = total_ms / args.steps
+    step_med, step_iqr = med_iqr(spread)
     # Every replay must reproduce the eager step bit for bit (the kernels are
     # deterministic and the step overwrites its outputs).
     for got, ref, name in zip((yd, dxd, dwd), eager, ("y", "dx", "dw")):
@@ -209,16 +276,19 @@ def main():
     for name, g in g_pass.items():
         g.replay()
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        marks[0].record()
+        for i in range(args.steps):
             g.replay()
-        e1.record()
+            marks[i + 1].record()
         torch.cuda.synchronize()
-        avg = e0.elapsed_time(e1) / (args.steps * PASS_REPS)
+        avg = marks[0].elapsed_time(marks[-1]) / (args.steps * PASS_REPS)
+        med, iqr = med_iqr([marks[i].elapsed_time(marks[i + 1]) / PASS_REPS
+                            for i in range(args.steps)])
         kernels[name] = {"avg_us": round(avg * 1e3, 2),
-                         "tflops": round(pass_units[name] * pass_flops / (avg * 1e-3) / 1e12, 2)}
+                         "median_us": round(med * 1e3, 2), "iqr_us": round(iqr * 1e3, 2),
+                         "tflops": round(pass_units[name] * pass_flops / (avg * 1e-3) / 1e12, 2),
+                         "gbps": round(pass_bytes[name] / (avg * 1e-3) / 1e9, 1)}
     kernels["bwd"]["launches"] = "direct_bwd_kernel (dX and dW blocks) + dw_split_reduce"
     kernels["bwd_data"]["note"] = "separate call, not part of the step"
     kernels["bwd_filter"]["note"] = "separate call, not part of the step"
@@ -243,6 +313,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_median": round(step_med, 4) if step_med is not None else None,
+        "ms_per_step_iqr": round(step_iqr, 4) if step_iqr is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -280,7 +352,7 @@ def main():
             mstep()
             torch.cuda.synchronize()
             reps = max(1, args.matmul_steps if n >= 2048 else 10 * args.matmul_steps)
-            mms = timed_steps(mstep, reps) / reps
+            mms = timed_steps(mstep, reps)[0] / reps
             mflops = 3 * 2 * n ** 3
             out["matmul"][str(n)] = {
                 "ms_per_step": round(mms, 4), "steps": reps,
@@ -320,8 +392,14 @@ def main():
             out["frontend_resident"] = {"error": proc.stderr.strip()[-300:]}
 
     if not args.no_cpu:
+        cpu_out = {}
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
-                                           step_flops / cfg["x"][0])
+                                           step_flops / cfg["x"][0], cpu_out)
+        if cpu_out:
+            # The eager step's outputs used the same inputs and G.
+            gpu_out = {"y": eager[0].cpu().numpy(), "dx": eager[1].cpu().numpy(),
+                       "dw": eager[2].cpu().numpy()}
+            out["accuracy"] = accuracy_report(cpu_out, gpu_out, st, pad)
     print(json.dumps(out), flush=True)
     return 0
 
