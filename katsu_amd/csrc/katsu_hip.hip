@@ -21,6 +21,7 @@
 #include "direct.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
+#include "pointwise.hpp"
 
 namespace katsu {
 namespace {
@@ -834,6 +835,119 @@ int bwd_fused_launch(const DirectFwdPlan &xp, DirectDwPlan wp, const float *x, c
 }
 
 // ---------------------------------------------------------------------------
+// 1x1 convolutions without padding (pw_kernel): every output pixel reads one
+// input pixel, so the three passes are plain GEMMs over gathered pixels.
+
+bool pw_ok(const ConvDims &d) {
+    return d.R == 1 && d.S == 1 && d.pad == 0 && d.npix_out > 0 && d.npix_out < kI32Max;
+}
+
+PwArgs pw_args(const ConvDims &d, int64_t m, int64_t n, int64_t k) {
+    PwArgs a{};
+    a.M = (int)m;
+    a.N = (int)n;
+    a.K = (int)k;
+    a.C = d.C;
+    a.H = d.H;
+    a.W = d.W;
+    a.KO = d.K;
+    a.OW = d.OW;
+    a.OHW = d.OHW;
+    a.HW = d.HW;
+    a.st = d.st;
+    a.x_img = d.CHW;
+    a.g_img = d.KOHW;
+    a.fd_ohw = fdiv(d.OHW);
+    a.fd_ow = fdiv(d.OW);
+    a.splits = 1;
+    a.kchunk = (int)((k + 31) / 32 * 32);
+    return a;
+}
+
+// 64-row tiles when they still give every CU a block, else 32.
+int pw_bm(int64_t m, int64_t n, int64_t splits) {
+    return cdiv(m, 64) * cdiv(n, 64) * splits >= kMinDirectBlocks ? 64 : 32;
+}
+
+template <int MODE, int BM>
+int pw_launch(PwArgs a, hipStream_t st) {
+    a.tiles_m = (int)cdiv(a.M, BM);
+    a.tiles_n = (int)cdiv(a.N, PwGeo<BM>::BN);
+    const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * a.splits;
+    if (blocks <= 0) return KATSU_OK;
+    if (blocks > kI32Max) return KATSU_E_INVALID;
+    pw_kernel<MODE, BM><<<dim3((unsigned)blocks), dim3(256), PwGeo<BM>::kBytes, st>>>(a);
+    return launch_status();
+}
+
+template <int MODE>
+int pw_run(const PwArgs &a, hipStream_t st) {
+    return pw_bm(a.M, a.N, a.splits) == 64 ? pw_launch<MODE, 64>(a, st)
+                                             : pw_launch<MODE, 32>(a, st);
+}
+
+int pw_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
+    PwArgs a = pw_args(d, d.K, d.npix_out, d.C);
+    a.x = x;
+    a.w = w;
+    a.out = y;
+    a.beta = 0.f;
+    return pw_run<0>(a, st);
+}
+
+int pw_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float beta,
+          hipStream_t st) {
+    PwArgs a = pw_args(d, d.C, d.npix_out, d.K);
+    a.g = gy;
+    a.w = w;
+    a.out = dx;
+    a.beta = beta;
+    return pw_run<1>(a, st);
+}
+
+// dW: the pixel reduction split so the launch has about two blocks per CU,
+// each split at least 256 pixels long.
+struct PwDwPlan {
+    bool ok = false;
+    int splits = 1, kchunk = 32;
+    int64_t pstride = 0;
+    size_t ws_bytes = 0;
+};
+
+PwDwPlan pw_dw_plan(const ConvDims &d) {
+    PwDwPlan pl;
+    if (!pw_ok(d)) return pl;
+    const int64_t kred = d.npix_out;
+    const int64_t tiles = cdiv(d.K, 32) * cdiv(d.C, 64);
+    int64_t splits = std::max<int64_t>(1, cdiv(2 * kMinDirectBlocks, tiles));
+    splits = std::min(splits, std::max<int64_t>(1, kred / 256));
+    const int64_t kchunk = cdiv(cdiv(kred, splits), 32) * 32;
+    splits = cdiv(kred, kchunk);
+    pl.ok = true;
+    pl.splits = (int)splits;
+    pl.kchunk = (int)kchunk;
+    pl.pstride = ((int64_t)d.K * d.C + 3) / 4 * 4;
+    pl.ws_bytes = splits > 1 ? (size_t)splits * (size_t)pl.pstride * sizeof(float) : 0;
+    return pl;
+}
+
+int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const PwDwPlan &pl,
+          float beta, float *ws, hipStream_t st) {
+    PwArgs a = pw_args(d, d.K, d.C, d.npix_out);
+    a.x = x;
+    a.g = gy;
+    const bool direct = pl.splits == 1;
+    a.out = direct ? dw : ws;
+    a.beta = direct ? beta : 0.f;
+    a.splits = pl.splits;
+    a.kchunk = pl.kchunk;
+    a.split_stride = direct ? 0 : pl.pstride;
+    const int rc = pw_run<2>(a, st);
+    if (rc != KATSU_OK || direct) return rc;
+    return launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
+}
+
+// ---------------------------------------------------------------------------
 // Forward.
 
 template <class C>
@@ -876,9 +990,15 @@ int conv_fwd_dev(const float *x, const float *w, float *y, const katsu_conv_geom
         int rc = KATSU_OK;
         if (direct_fwd<0>(P, st, &rc)) return rc;
     }
+    if (pw_ok(d)) return pw_fwd(x, w, y, d, st);
+    // The largest tile that still gives every CU a block (rows x pixels).
+    const int64_t px = d.npix_out;
     if (d.K <= 16) return fwd_cfg<CfgS>(x, w, y, d, st);
-    if (d.K <= 64) return fwd_cfg<CfgM>(x, w, y, d, st);
-    return fwd_cfg<CfgL>(x, w, y, d, st);
+    if (d.K > 64 && cdiv(d.K, 128) * cdiv(px, 128) >= kMinDirectBlocks)
+        return fwd_cfg<CfgL>(x, w, y, d, st);
+    if (cdiv(d.K, 64) * cdiv(px, 128) >= kMinDirectBlocks) return fwd_cfg<CfgM>(x, w, y, d, st);
+    if (cdiv(d.K, 64) * cdiv(px, 64) >= kMinDirectBlocks) return fwd_cfg<Cfg64>(x, w, y, d, st);
+    return fwd_cfg<Cfg32>(x, w, y, d, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -964,6 +1084,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     int rc = KATSU_OK;
     if (dx_as_forward(d, gy, w, dx, beta, &P) && direct_fwd<1>(P, st, &rc)) return rc;
     if (dx_superpixel(d, gy, w, dx, beta, st, &rc)) return rc;
+    if (pw_ok(d)) return pw_dx(gy, w, dx, d, beta, st);
     if (d.C <= 16) return dx_cfg<CfgS>(gy, w, dx, d, beta, st);
     if (d.C <= 64) return dx_cfg<CfgM>(gy, w, dx, d, beta, st);
     return dx_cfg<CfgL>(gy, w, dx, d, beta, st);
@@ -977,6 +1098,7 @@ struct DwPlan {
     int64_t pstride;  // floats between partials (a multiple of 4)
     size_t ws_bytes;
     DirectDwPlan direct;  // used when direct.ok
+    PwDwPlan pw;          // used when pw.ok (1x1, no padding)
 };
 
 template <class C>
@@ -1007,6 +1129,13 @@ DwPlan dw_plan_any(const ConvDims &d) {
         DwPlan pl{};
         pl.ws_bytes = dp.ws_bytes;
         pl.direct = dp;
+        return pl;
+    }
+    const PwDwPlan pp = pw_dw_plan(d);
+    if (pp.ok) {
+        DwPlan pl{};
+        pl.ws_bytes = pp.ws_bytes;
+        pl.pw = pp;
         return pl;
     }
     return dw_plan<CfgW>(d);
@@ -1079,6 +1208,7 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
         }
     }
     if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
+    if (pl.pw.ok) return pw_dw(x, gy, dw, d, pl.pw, beta, wsp, st);
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 

@@ -1,0 +1,267 @@
+// pointwise.hpp -- 1x1 convolutions (any stride, no padding) as fp32 MFMA
+// GEMMs whose pixel operand is addressed in place: the forward
+// (conv2d.rs:95-115) and both backward passes (backward_buffers,
+// conv2d.rs:265-292) of Conv2D for R = S = 1.  With one tap, every output
+// pixel (oy, ox) reads exactly input pixel (oy*s, ox*s), so
+//
+//   MODE 0  forward  y[n][o][p]  = sum_c w[o][c] x[n][c][oy*s][ox*s]
+//           i = o (M = K), j = output pixel over the batch (N*OH*OW), k = c
+//   MODE 1  dX       dx[n][c][oy*s][ox*s] = sum_o w[o][c] G[n][o][p]
+//           i = c (M = C), j = output pixel, k = o; the other s*s - 1 input
+//           pixels of the s x s block that (oy, ox) owns receive no tap and
+//           are written as zeros in the same epilogue
+//   MODE 2  dW       dw[o][c] = sum_{n,p} G[n][o][p] x[n][c][oy*s][ox*s]
+//           i = o (M = K), j = c (N = C), k = output pixel, split over k
+//           into fixed partial slices (summed by dw_split_reduce)
+//
+// Block tile BM x 64 x 32 (BM 64 or 32), four waves in a 2 x 2 grid of
+// (BM/2) x 32 wave tiles.  Both operands are staged through registers into
+// LDS as [k][i] and [k][j] (i and j contiguous), double-buffered, and read
+// FM (FN) fragments at a time: fragment a's MFMA row m is tile row FM*m + a.
+// Each thread loads elements along the operand's coalesced dimension: pixel
+// columns for the gathered x and G operands of MODE 0 and 1 (fixed per
+// thread, so their addresses are decoded once), pixels along k in MODE 2
+// (one pixel per thread per k-tile), the weight's contiguous dimension
+// otherwise.
+#pragma once
+
+#include "direct.hpp"
+
+namespace katsu {
+
+struct PwArgs {
+    const float *x, *w, *g;
+    float *out;          // y (MODE 0), dx (MODE 1), dw or the partial slices (MODE 2)
+    int M, N, K;         // GEMM sizes as above
+    int C, H, W, KO, OW, OHW, HW, st;
+    int64_t x_img, g_img;  // C*H*W and KO*OH*OW
+    int tiles_m, tiles_n, splits, kchunk;  // kchunk: a multiple of 32
+    int64_t split_stride;  // floats between partial slices, or 0 when writing the output
+    float beta;            // out = beta*out + result when writing the output directly
+    FastDiv fd_ohw, fd_ow;
+};
+
+template <int BM>
+struct PwGeo {
+    static constexpr int BN = 64, BK = 32;
+    static constexpr int PA = BM + 4, PB = BN + 4;  // [k][i] and [k][j] row pitches
+    static constexpr int SA = BK * PA, SB = BK * PB;
+    static constexpr int STAGE = SA + SB;
+    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+};
+
+template <int MODE, int BM>
+__global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
+    using Geo = PwGeo<BM>;
+    constexpr int BN = Geo::BN, BK = Geo::BK;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr int NA = BM * BK / 256, NB = BN * BK / 256;  // elements per thread per k-tile
+    static_assert(BM == 32 || BM == 64, "BM");
+
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wi0 = (wave >> 1) * WM, wj0 = (wave & 1) * WN;
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int split = t / (g.tiles_m * g.tiles_n);
+    const int tile = t - split * (g.tiles_m * g.tiles_n);
+    const int i0 = (tile % g.tiles_m) * BM, j0 = (tile / g.tiles_m) * BN;
+    const int kb = split * g.kchunk;
+    const int ke = min(kb + g.kchunk, g.K);
+
+    // Element e = q*256 + tid of a tile.  "Fast" dimension = the one that
+    // varies across consecutive threads.
+    //   MODE 0: A (o, c) c-fast; B (c, pixel) pixel-fast
+    //   MODE 1: A (c, o) c-fast (i-fast); B (o, pixel) pixel-fast
+    //   MODE 2: A (o, pixel) pixel-fast (k-fast); B (pixel, c) pixel-fast (k-fast)
+    // Pixel columns of MODE 0 and 1: this thread's column is j0 + tid % 64.
+    int64_t colx = 0, colg = 0;
+    bool colok = false;
+    if (MODE != 2) {
+        const int j = j0 + (tid & 63);
+        colok = j < g.N;
+        const int jj = colok ? j : 0;
+        const int n = g.fd_ohw.div(jj);
+        const int p = jj - n * g.OHW;
+        const int oy = g.fd_ow.div(p);
+        const int ox = p - oy * g.OW;
+        colx = (int64_t)n * g.x_img + (int64_t)oy * g.st * g.W + (int64_t)ox * g.st;
+        colg = (int64_t)n * g.g_img + p;
+    }
+
+    float va[NA], vb[NB];
+    auto load = [&](int k0) __attribute__((always_inline)) {
+        if (MODE == 0) {
+#pragma unroll
+            for (int q = 0; q < NA; ++q) {  // w[o][c], c fastest
+                const int e = q * 256 + tid;
+                const int i = i0 + e / BK, k = k0 + e % BK;
+                va[q] = (i < g.M && k < ke) ? g.w[(int64_t)i * g.C + k] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < NB; ++q) {  // x[n][c][oy*s][ox*s]
+                const int k = k0 + q * 4 + (tid >> 6);
+                vb[q] = (colok && k < ke) ? g.x[colx + (int64_t)k * g.HW] : 0.f;
+            }
+        } else if (MODE == 1) {
+#pragma unroll
+            for (int q = 0; q < NA; ++q) {  // w[o][c], c fastest
+                const int e = q * 256 + tid;
+                const int i = i0 + e % BM, k = k0 + e / BM;
+                va[q] = (i < g.M && k < ke) ? g.w[(int64_t)k * g.C + i] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < NB; ++q) {  // G[n][o][p]
+                const int k = k0 + q * 4 + (tid >> 6);
+                vb[q] = (colok && k < ke) ? g.g[colg + (int64_t)k * g.OHW] : 0.f;
+            }
+        } else {
+            // One pixel per thread per k-tile: k = k0 + tid % 32.
+            const int k = k0 + (tid & (BK - 1));
+            const bool kok = k < ke;
+            const int kk = kok ? k : 0;
+            const int n = g.fd_ohw.div(kk);
+            const int p = kk - n * g.OHW;
+            const int oy = g.fd_ow.div(p);
+            const int ox = p - oy * g.OW;
+            const int64_t gb = (int64_t)n * g.g_img + p;
+            const int64_t xb = (int64_t)n * g.x_img + (int64_t)oy * g.st * g.W + (int64_t)ox * g.st;
+#pragma unroll
+            for (int q = 0; q < NA; ++q) {  // G[n][o][p]
+                const int i = i0 + q * (256 / BK) + (tid / BK);
+                va[q] = (kok && i < g.M) ? g.g[gb + (int64_t)i * g.OHW] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < NB; ++q) {  // x[n][c][oy*s][ox*s]
+                const int j = j0 + q * (256 / BK) + (tid / BK);
+                vb[q] = (kok && j < g.N) ? g.x[xb + (int64_t)j * g.HW] : 0.f;
+            }
+        }
+    };
+    auto store = [&](float *st) __attribute__((always_inline)) {
+        float *sa = st, *sb = st + Geo::SA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+            const int e = q * 256 + tid;
+            int i, k;
+            if (MODE == 0) { i = e / BK; k = e % BK; }
+            else if (MODE == 1) { i = e % BM; k = e / BM; }
+            else { i = q * (256 / BK) + tid / BK; k = tid & (BK - 1); }
+            sa[k * Geo::PA + i] = va[q];
+        }
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            int j, k;
+            if (MODE != 2) { j = tid & 63; k = q * 4 + (tid >> 6); }
+            else { j = q * (256 / BK) + tid / BK; k = tid & (BK - 1); }
+            sb[k * Geo::PB + j] = vb[q];
+        }
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Step s of 16-deep block kq: lane group lg takes k = 16*kq + 4*lg + s.
+    auto compute = [&](const float *st) __attribute__((always_inline)) {
+        const float *sa = st, *sb = st + Geo::SA;
+#pragma unroll
+        for (int kq = 0; kq < BK / 16; ++kq)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int k = 16 * kq + 4 * lg + s;
+                const auto av = *reinterpret_cast<const typename FloatN<FM>::T *>(
+                    sa + k * Geo::PA + wi0 + FM * l16);
+                const auto bv = *reinterpret_cast<const typename FloatN<FN>::T *>(
+                    sb + k * Geo::PB + wj0 + FN * l16);
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int b = 0; b < FN; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            lane_of<FM>(av, a), lane_of<FN>(bv, b), acc[a][b], 0, 0, 0);
+            }
+    };
+
+    if (kb < ke) {
+        float *st0 = smem, *st1 = smem + Geo::STAGE;
+        load(kb);
+        store(st0);
+        __syncthreads();
+        for (int k0 = kb; k0 < ke; k0 += 2 * BK) {
+            const bool m1 = k0 + BK < ke, m2 = k0 + 2 * BK < ke;
+            if (m1) load(k0 + BK);
+            compute(st0);
+            if (m1) store(st1);
+            __syncthreads();
+            if (!m1) break;
+            if (m2) load(k0 + 2 * BK);
+            compute(st1);
+            if (m2) store(st0);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: fragment (a, b), register v is tile row FM*(4*lg + v) + a,
+    // tile column FN*l16 + b.
+    const bool direct = g.split_stride == 0;
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int j = j0 + wj0 + FN * l16 + b;
+        if (j >= g.N) continue;
+        if (MODE == 2) {
+            float *out = direct ? g.out : g.out + (int64_t)split * g.split_stride;
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = i0 + wi0 + FM * (4 * lg + v) + a;
+                    if (i >= g.M) continue;
+                    float *p = out + (int64_t)i * g.N + j;
+                    *p = (direct && g.beta != 0.f) ? *p + acc[a][b][v] : acc[a][b][v];
+                }
+            continue;
+        }
+        const int n = g.fd_ohw.div(j);
+        const int p = j - n * g.OHW;
+        if (MODE == 0) {
+            float *col = g.out + (int64_t)n * g.g_img + p;
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = i0 + wi0 + FM * (4 * lg + v) + a;
+                    if (i < g.M) store_beta(col + (int64_t)i * g.OHW, acc[a][b][v], g.beta);
+                }
+        } else {
+            // The s x s input block of output pixel (oy, ox), clipped to the
+            // image: the tap's value at its corner, zeros elsewhere (kept as
+            // they are when accumulating).
+            const int oy = g.fd_ow.div(p);
+            const int ox = p - oy * g.OW;
+            const int iy = oy * g.st, ix = ox * g.st;
+            const int hy = min(g.st, g.H - iy), hx = min(g.st, g.W - ix);
+            float *col = g.out + (int64_t)n * g.x_img + (int64_t)iy * g.W + ix;
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = i0 + wi0 + FM * (4 * lg + v) + a;
+                    if (i >= g.M) continue;
+                    float *blk = col + (int64_t)i * g.HW;
+                    store_beta(blk, acc[a][b][v], g.beta);
+                    if (g.beta == 0.f) {
+                        for (int dy = 0; dy < hy; ++dy)
+                            for (int dx = 0; dx < hx; ++dx)
+                                if (dy | dx) blk[dy * g.W + dx] = 0.f;
+                    }
+                }
+        }
+    }
+}
+
+}  // namespace katsu
