@@ -61,22 +61,31 @@ __device__ __forceinline__ float lane_of(const typename FloatN<N>::T &v, int i) 
     else return v[i];
 }
 
-template <int BM, int BN, int BK_, bool TA, bool TB>
-__global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
+// WG wave groups of four waves share a block tile: group g takes the tile's
+// k-tiles g, g + WG, ... through LDS stages of its own, and the groups' sums
+// are added in group order at the end.  Two groups keep two waves on every
+// SIMD when the grid has only about one block per CU.
+template <int BM, int BN, int BK_, bool TA, bool TB, int WG>
+__global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g) {
     using Geo = GemmGeo<BM, BN, BK_, TA, TB>;
+    static_assert(WG == 1 || WG == 2, "one or two wave groups");
     constexpr int BK = Geo::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 16, FN = WN / 16;
+    static_assert(WG == 1 || FM * FN * 4 * 256 <= 2 * WG * Geo::STAGE,
+                  "the group hand-off fits in the stages");
     static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
     static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
     constexpr int A4 = BM * BK / 4 / 256;  // float4 loads per thread per tile
     constexpr int B4 = BN * BK / 4 / 256;
     static_assert(A4 >= 1 && B4 >= 1, "tile too small for 256 threads");
 
-    extern __shared__ float smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ float smem_all[];
+    const int tid = threadIdx.x & 255, grp = threadIdx.x >> 8;
+    const int lane = tid & 63, wave = tid >> 6;
     const int wi0 = (wave >> 1) * WM, wj0 = (wave & 1) * WN;
     const int l16 = lane & 15, lg = lane >> 4;
+    float *smem = smem_all + grp * 2 * Geo::STAGE;
 
     const int t = xcd_swizzle(blockIdx.x, gridDim.x);
     const int split = t / (g.tiles_m * g.tiles_n);
@@ -147,74 +156,124 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const GemmArgs g) {
 #pragma unroll
         for (int b = 0; b < FN; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // The BK-deep tile of a stage: BK/16 blocks of four MFMA steps per
-    // fragment pair.
-    auto compute = [&](const float *st) __attribute__((always_inline)) {
+    // The fragments of one 16-deep k block: step s of lane group lg is
+    // k = 16*kq + 4*lg + s.
+    struct Frag {
+        float a[4][FM], b[4][FN];
+    };
+    auto read = [&](const float *st, int kq, Frag &fr) __attribute__((always_inline)) {
         const float *sa = st, *sb = st + Geo::SA;
+        if (!TA) {
 #pragma unroll
-        for (int kq = 0; kq < BK / 16; ++kq) {
-            floatx4 ak[FM], bk[FN];  // k-contiguous operands: four steps per read
-            if (!TA) {
+            for (int a = 0; a < FM; ++a) {
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(
+                    sa + (wi0 + 16 * a + l16) * Geo::PA + 16 * kq + 4 * lg);
 #pragma unroll
-                for (int a = 0; a < FM; ++a)
-                    ak[a] = *reinterpret_cast<const floatx4 *>(
-                        sa + (wi0 + 16 * a + l16) * Geo::PA + 16 * kq + 4 * lg);
+                for (int s = 0; s < 4; ++s) fr.a[s][a] = v[s];
             }
-            if (TB) {
-#pragma unroll
-                for (int b = 0; b < FN; ++b)
-                    bk[b] = *reinterpret_cast<const floatx4 *>(
-                        sb + (wj0 + 16 * b + l16) * Geo::PB + 16 * kq + 4 * lg);
-            }
+        } else {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const int k = 16 * kq + 4 * lg + s;
-                float af[FM], bf[FN];
-                if (!TA) {
+                const auto v = *reinterpret_cast<const typename FloatN<FM>::T *>(
+                    sa + (16 * kq + 4 * lg + s) * Geo::PA + wi0 + FM * l16);
 #pragma unroll
-                    for (int a = 0; a < FM; ++a) af[a] = ak[a][s];
-                } else {
-                    const auto v = *reinterpret_cast<const typename FloatN<FM>::T *>(
-                        sa + k * Geo::PA + wi0 + FM * l16);
+                for (int a = 0; a < FM; ++a) fr.a[s][a] = lane_of<FM>(v, a);
+            }
+        }
+        if (TB) {
 #pragma unroll
-                    for (int a = 0; a < FM; ++a) af[a] = lane_of<FM>(v, a);
-                }
-                if (TB) {
+            for (int b = 0; b < FN; ++b) {
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(
+                    sb + (wj0 + 16 * b + l16) * Geo::PB + 16 * kq + 4 * lg);
 #pragma unroll
-                    for (int b = 0; b < FN; ++b) bf[b] = bk[b][s];
-                } else {
-                    const auto v = *reinterpret_cast<const typename FloatN<FN>::T *>(
-                        sb + k * Geo::PB + wj0 + FN * l16);
+                for (int s = 0; s < 4; ++s) fr.b[s][b] = v[s];
+            }
+        } else {
 #pragma unroll
-                    for (int b = 0; b < FN; ++b) bf[b] = lane_of<FN>(v, b);
-                }
+            for (int s = 0; s < 4; ++s) {
+                const auto v = *reinterpret_cast<const typename FloatN<FN>::T *>(
+                    sb + (16 * kq + 4 * lg + s) * Geo::PB + wj0 + FN * l16);
 #pragma unroll
-                for (int a = 0; a < FM; ++a)
-#pragma unroll
-                    for (int b = 0; b < FN; ++b)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b],
-                                                                         0, 0, 0);
+                for (int b = 0; b < FN; ++b) fr.b[s][b] = lane_of<FN>(v, b);
             }
         }
     };
+    auto mma = [&](const Frag &fr) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fr.a[s][a], fr.b[s][b],
+                                                                     acc[a][b], 0, 0, 0);
+    };
+    // LDS reads per k block (b128 for k-contiguous operands, one FloatN per
+    // step otherwise) and MFMAs per k block.
+    constexpr int RD = (TA ? 4 : FM) + (TB ? FN : 4);
+    constexpr int MF = 4 * FM * FN;
+    // The BK-deep tile of a stage, software-pipelined: the fragments of k
+    // block kq+1 are read while kq's MFMAs run, so a wave alone on its SIMD
+    // (one block per CU) still keeps the matrix pipe busy.
+    auto compute = [&](const float *st) __attribute__((always_inline)) {
+        constexpr int NKQ = BK / 16;
+        Frag f0, f1;
+        read(st, 0, f0);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int kq = 0; kq < NKQ; kq += 2) {
+            if (kq + 1 < NKQ) read(st, kq + 1, f1);
+            mma(f0);
+            order_reads_then_mfma<RD, MF>();
+            if (kq + 1 >= NKQ) break;
+            if (kq + 2 < NKQ) read(st, kq + 2, f0);
+            mma(f1);
+            order_reads_then_mfma<RD, MF>();
+        }
+    };
 
-    if (kb < ke) {
+    // Rounds of WG k-tiles; every group runs every round (a k-tile past the
+    // end loads as zeros), so the block's barriers stay matched.
+    const int nrounds = kb < ke ? (int)((ke - kb + WG * BK - 1) / (WG * BK)) : 0;
+    auto kof = [&](int r) { return kb + (r * WG + grp) * BK; };
+    if (nrounds > 0) {
         float *st0 = smem, *st1 = smem + Geo::STAGE;
-        load(kb);
+        load(kof(0));
         store(st0);
         __syncthreads();
-        for (int k0 = kb; k0 < ke; k0 += 2 * BK) {
-            const bool m1 = k0 + BK < ke, m2 = k0 + 2 * BK < ke;
-            if (m1) load(k0 + BK);
+        for (int r = 0; r < nrounds; r += 2) {
+            const bool m1 = r + 1 < nrounds, m2 = r + 2 < nrounds;
+            if (m1) load(kof(r + 1));
             compute(st0);
             if (m1) store(st1);
             __syncthreads();
             if (!m1) break;
-            if (m2) load(k0 + 2 * BK);
+            if (m2) load(kof(r + 2));
             compute(st1);
             if (m2) store(st0);
             __syncthreads();
         }
+    }
+    if constexpr (WG == 2) {
+        // Group 1 hands its sums to group 0 through LDS (the stages are
+        // free after the last barrier): value idx of thread tid at idx*256 + tid.
+        float *red = smem_all;
+        if (grp == 1) {
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) red[((a * FN + b) * 4 + v) * 256 + tid] = acc[a][b][v];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[a][b][v] += red[((a * FN + b) * 4 + v) * 256 + tid];
     }
 
     // Epilogue: fragment (a, b), register v is row m = 4*lg + v, column n = l16.

@@ -182,20 +182,32 @@ int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstri
                         float beta, hipStream_t st);
 State &state();
 
-template <int BM, int BN, int BK, bool TA, bool TB>
+// Raises a kernel's dynamic LDS limit above 64 KiB (defined below).
+template <auto Kernel>
+int lds_optin(size_t bytes);
+
+template <int BM, int BN, int BK, bool TA, bool TB, int WG>
 int gemm_fast_launch(const GemmArgs &g, int64_t blocks, hipStream_t st) {
     using Geo = GemmGeo<BM, BN, BK, TA, TB>;
-    constexpr auto kern = gemm_kernel<BM, BN, BK, TA, TB>;
-    kern<<<dim3((unsigned)blocks), dim3(256), Geo::kBytes, st>>>(g);
+    constexpr auto kern = gemm_kernel<BM, BN, BK, TA, TB, WG>;
+    const int rc = lds_optin<kern>(WG * Geo::kBytes);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3((unsigned)blocks), dim3(256 * WG), WG * Geo::kBytes, st>>>(g);
     return launch_status();
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int WG>
 int gemm_fast_t(const GemmArgs &g, int64_t blocks, int ta, int tb, hipStream_t st) {
-    if (!ta && !tb) return gemm_fast_launch<BM, BN, BK, false, false>(g, blocks, st);
-    if (!ta && tb) return gemm_fast_launch<BM, BN, BK, false, true>(g, blocks, st);
-    if (ta && !tb) return gemm_fast_launch<BM, BN, BK, true, false>(g, blocks, st);
-    return gemm_fast_launch<BM, BN, BK, true, true>(g, blocks, st);
+    if (!ta && !tb) return gemm_fast_launch<BM, BN, BK, false, false, WG>(g, blocks, st);
+    if (!ta && tb) return gemm_fast_launch<BM, BN, BK, false, true, WG>(g, blocks, st);
+    if (ta && !tb) return gemm_fast_launch<BM, BN, BK, true, false, WG>(g, blocks, st);
+    return gemm_fast_launch<BM, BN, BK, true, true, WG>(g, blocks, st);
+}
+
+template <int BM, int BN, int BK>
+int gemm_fast_wg(const GemmArgs &g, int64_t blocks, int wg, int ta, int tb, hipStream_t st) {
+    return wg == 2 ? gemm_fast_t<BM, BN, BK, 2>(g, blocks, ta, tb, st)
+                   : gemm_fast_t<BM, BN, BK, 1>(g, blocks, ta, tb, st);
 }
 
 // Tile choice: the largest square tile (128, 64, 32) that gives every CU a
@@ -208,6 +220,9 @@ int gemm_fast_t(const GemmArgs &g, int64_t blocks, int ta, int tb, hipStream_t s
 #endif
 #ifndef KATSU_GEMM_BK64
 #define KATSU_GEMM_BK64 64
+#endif
+#ifndef KATSU_GEMM_WG2_BELOW
+#define KATSU_GEMM_WG2_BELOW 512
 #endif
 
 // The dedicated GEMM (gemm.hpp) for aligned problems, with a fixed-order
@@ -265,9 +280,12 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     g.c = splits > 1 ? ws : c;
     g.split_stride = splits > 1 ? pstride : 0;
     const int64_t blocks = tiles * splits;
-    *rc = T == 128  ? gemm_fast_t<128, 128, 16>(g, blocks, ta, tb, st)
-          : T == 64 ? gemm_fast_t<64, 64, KATSU_GEMM_BK64>(g, blocks, ta, tb, st)
-                    : gemm_fast_t<32, 32, 32>(g, blocks, ta, tb, st);
+    // Fewer blocks than two per CU: two wave groups per block, so every SIMD
+    // still holds two waves.
+    const int wg = blocks < KATSU_GEMM_WG2_BELOW ? 2 : 1;
+    *rc = T == 128  ? gemm_fast_wg<128, 128, 16>(g, blocks, wg, ta, tb, st)
+          : T == 64 ? gemm_fast_wg<64, 64, KATSU_GEMM_BK64>(g, blocks, wg, ta, tb, st)
+                    : gemm_fast_wg<32, 32, 32>(g, blocks, wg, ta, tb, st);
     if (*rc == KATSU_OK && splits > 1)
         *rc = launch_split_reduce(ws, c, M * N, pstride, (int)splits, beta, st);
     return true;
