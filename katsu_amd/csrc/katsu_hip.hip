@@ -22,6 +22,7 @@
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "pointwise.hpp"
+#include "smallc.hpp"
 
 namespace katsu {
 namespace {
@@ -966,6 +967,57 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
 }
 
 // ---------------------------------------------------------------------------
+// The stem forward (stem_fwd_kernel): three input channels, 7x7, rows of at
+// most 112 output pixels.
+
+constexpr int kStemF = 7, kStemPitch = 256;
+
+bool stem_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st,
+              int *rc) {
+    using Geo = StemGeo<3, 7, 7, kStemPitch>;
+    if (d.C != 3 || d.R != 7 || d.S != 7) return false;
+    // Whole rows of 64..112 pixels; the padded tap s = 7 reads one column
+    // past the halo, which must still lie inside the row pitch.
+    if (d.OW < 64 || d.OW > 16 * kStemF || (int64_t)(d.OW - 1) * d.st + Geo::SP > kStemPitch)
+        return false;
+    if ((int64_t)d.CHW * 4 >= (int64_t)kMaxBufBytes ||
+        (int64_t)d.K * d.CRS * 4 >= (int64_t)kMaxBufBytes)
+        return false;
+    const int64_t co_blocks = cdiv(d.K, 64);
+    // About one block per CU: rows per block, even (two groups).
+    int64_t rb = std::max<int64_t>(2, cdiv(co_blocks * d.N * d.OH, kMinDirectBlocks));
+    rb += rb & 1;
+    const int64_t blocks_img = cdiv(d.OH, rb);
+    const int64_t blocks = co_blocks * d.N * blocks_img;
+    if (blocks > kI32Max) return false;
+    StemArgs a;
+    a.x = x;
+    a.w = w;
+    a.y = y;
+    a.N = d.N;
+    a.C = d.C;
+    a.H = d.H;
+    a.W = d.W;
+    a.K = d.K;
+    a.OH = d.OH;
+    a.OW = d.OW;
+    a.st = d.st;
+    a.pad = d.pad;
+    a.x_img = d.CHW;
+    a.y_img = d.KOHW;
+    a.rows_per_block = (int)rb;
+    a.blocks_img = (int)blocks_img;
+    a.co_blocks = (int)co_blocks;
+    a.ncols = (d.OW - 1) * d.st + d.S;
+    a.w_bytes = (uint32_t)((int64_t)d.K * d.CRS * 4);
+    constexpr auto kern = stem_fwd_kernel<3, 7, 7, kStemF, kStemPitch>;
+    if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
+    kern<<<dim3((unsigned)blocks), dim3(512), Geo::kBytes, st>>>(a);
+    *rc = launch_status();
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // Forward.
 
 template <class C>
@@ -1007,6 +1059,7 @@ int conv_fwd_dev(const float *x, const float *w, float *y, const katsu_conv_geom
                            d.OH, d.OW, 0.f};
         int rc = KATSU_OK;
         if (direct_fwd<0>(P, st, &rc)) return rc;
+        if (stem_fwd(x, w, y, d, st, &rc)) return rc;
     }
     if (pw_ok(d)) return pw_fwd(x, w, y, d, st);
     // The largest tile that still gives every CU a block (rows x pixels).

@@ -1,0 +1,210 @@
+// smallc.hpp -- the forward of convolutions with three input channels and a
+// 7x7 filter, any stride and padding (the stem layer of config 5):
+// Conv2D::forward (conv2d.rs:95-115), y = sum over (c, r, s) of
+// w[o][c][r][s] * x[c][oy*st - pad + r][ox*st - pad + s].
+//
+// GEMM view: i = output channel (64 per block), j = output pixel (one image
+// row per step), k = (c, r, s) with s padded to 8.  A k-step of four takes
+// taps s = 4h .. 4h+3 of one (c, r), lane group lg (lanes 16lg..16lg+15)
+// taking s = 4h + lg.  Every LDS address is then a per-lane base (the lane's
+// pixel column plus lg) plus a compile-time step offset; the lane groups of a
+// stride-2 read fall on distinct banks; and the padding costs 8/7 of the
+// MFMAs (three channels in quads, as the general direct kernel stages them,
+// would cost 4/3).
+//
+// A block is 512 threads: two groups of four waves that share the filter in
+// LDS (64 x 3*7*8 floats, staged once) and each walk their own output rows
+// (group g takes rows r0 + g, r0 + g + 2, ...) through a double-buffered
+// halo of 7 input rows per channel.  Wave q of a group owns output channels
+// 16q .. 16q+15 and the whole row (F fragments of 16 pixels).  A row's output
+// is stored straight from the accumulators after the barrier that ends its
+// step, so the stores drain while the next row computes.
+#pragma once
+
+#include "direct.hpp"
+
+namespace katsu {
+
+struct StemArgs {
+    const float *x, *w;
+    float *y;
+    int N, C, H, W, K, OH, OW, st, pad;
+    int64_t x_img, y_img;  // C*H*W, K*OH*OW
+    int rows_per_block;    // even: the two groups take alternate rows
+    int blocks_img;        // cdiv(OH, rows_per_block)
+    int co_blocks;         // cdiv(K, 64)
+    int ncols;             // (OW - 1)*st + S: halo columns (<= PITCH)
+    uint32_t w_bytes;
+};
+
+template <int CC, int R, int S, int PITCH>
+struct StemGeo {
+    static constexpr int SP = 8;                 // s padded to two halves of four
+    static constexpr int WK = CC * R * SP;       // k extent of a filter row
+    static constexpr int WP = WK + 2;            // == 2 (mod 4): a half-wave's A reads on 32 banks
+    static constexpr int WS = (64 * WP + 255) / 256 * 256;
+    static constexpr int CP = R * PITCH;         // halo channel pitch
+    static constexpr int HS = CC * CP;           // one halo stage
+    static constexpr int TOTAL = WS + 4 * HS;    // filter + two groups x two stages
+    static constexpr size_t kBytes = (size_t)TOTAL * sizeof(float);
+    static_assert(S <= SP && PITCH % 64 == 0, "stem geometry");
+};
+
+template <int CC, int R, int S, int F, int PITCH>
+__global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
+    using Geo = StemGeo<CC, R, S, PITCH>;
+    constexpr int SP = Geo::SP;
+    constexpr int NK = CC * R * 2;  // k-steps of a row
+    constexpr int LPR = PITCH / 64;
+
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x;
+    const int grp = tid >> 8, wq = (tid >> 6) & 3, lane = tid & 63;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index in the block
+
+    const int b = blockIdx.x;
+    const int cb = b % a.co_blocks;
+    const int rest = b / a.co_blocks;
+    const int n = rest / a.blocks_img;
+    const int r0 = (rest - n * a.blocks_img) * a.rows_per_block;
+    const int co0 = cb * 64;
+    const int nsteps = a.rows_per_block / 2;  // rows per group
+
+    float *ws = smem;
+    float *hs0 = smem + Geo::WS + grp * 2 * Geo::HS;
+    float *hs1 = hs0 + Geo::HS;
+
+    const __amdgpu_buffer_rsrc_t rx =
+        buf_rsrc(a.x + (int64_t)n * a.x_img, (uint32_t)(a.x_img * 4));
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, a.w_bytes);
+
+    // The filter: row o of the LDS copy holds w[co0 + o][c][r][s] at
+    // (c*R + r)*8 + s, zeros for s >= S and for channels past K.
+    {
+        constexpr int NI = Geo::WS / 64;
+        for (int i = wv; i < NI; i += 8) {
+            const int e = i * 64 + lane;
+            const int row = e / Geo::WP, col = e - (e / Geo::WP) * Geo::WP;
+            const int c = col / (R * SP), rs = col - c * (R * SP);
+            const int r = rs / SP, s = rs - r * SP;
+            const int co = co0 + row;
+            const bool ok = row < 64 && co < a.K && col < Geo::WK && s < S;
+            lds_dma_b32(rw, ws + i * 64, ok ? (((co * CC + c) * R + r) * S + s) * 4 : kOOB);
+        }
+    }
+    // Halo of output row oy: channel c, row r, column col at c*CP + r*PITCH +
+    // col; image column col - pad, zeros outside the image (and for rows past
+    // the output, whose results are not stored).  Wave q of a group stages
+    // columns 64q .. 64q+63 of every (c, r) row: one LDS-direct load each,
+    // with the lane's column offset fixed and the row offsets compile-time.
+    static_assert(LPR == 4, "one 64-column chunk per wave of a group");
+    const int q = wv & 3;
+    int colq;
+    {
+        const int col = q * 64 + lane;
+        const int ix = col - a.pad;
+        colq = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
+    }
+    const int rowbytes = a.W * 4, chanbytes = a.H * a.W * 4;
+    auto stage = [&](float *hs, int oy) __attribute__((always_inline)) {
+        const int iy0 = oy * a.st - a.pad;
+        const bool rowok = oy < a.OH;
+#pragma unroll
+        for (int c = 0; c < CC; ++c)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int iy = iy0 + r;
+                const bool ok = rowok && (unsigned)iy < (unsigned)a.H;
+                // colq may be kOOB: kOOB plus a row offset (< 1 GiB) stays out of range.
+                lds_dma_b32(rx, hs + c * Geo::CP + r * PITCH + q * 64,
+                            ok ? c * chanbytes + iy * rowbytes + colq : kOOB);
+            }
+    };
+
+    // Per-lane bases: B, the lane's pixel column plus its tap lg; A, the
+    // lane's output channel row plus lg.
+    int pix[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const int ox = min(f * 16 + l16, a.OW - 1);
+        pix[f] = ox * a.st + lg;
+    }
+    const int abase = (wq * 16 + l16) * Geo::WP + lg;
+
+    floatx4 acc[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) acc[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto fetch = [&](const float *hs, const int kk, float (&bv)[F], float &av)
+        __attribute__((always_inline)) {
+        const int c = kk / (2 * R), r = (kk / 2) % R, h = kk % 2;
+        av = ws[abase + (c * R + r) * SP + 4 * h];
+        const int toff = c * Geo::CP + r * PITCH + 4 * h;
+#pragma unroll
+        for (int f = 0; f < F; ++f) bv[f] = hs[pix[f] + toff];
+    };
+    auto mma = [&](const float (&bv)[F], const float av) __attribute__((always_inline)) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[f], acc[f], 0, 0, 0);
+    };
+    auto compute = [&](const float *hs) __attribute__((always_inline)) {
+        float b0[F], b1[F];
+        float a0, a1;
+        fetch(hs, 0, b0, a0);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int kk = 0; kk < NK; kk += 2) {
+            if (kk + 1 < NK) fetch(hs, kk + 1, b1, a1);
+            mma(b0, a0);
+            order_reads_then_mfma<F + 1, F>();
+            if (kk + 2 < NK) fetch(hs, kk + 2, b0, a0);
+            if (kk + 1 < NK) mma(b1, a1);
+            order_reads_then_mfma<F + 1, F>();
+        }
+    };
+    // Fragment f, register v: output channel 4*lg + v of the wave's 16,
+    // pixel 16f + l16 of the row.
+    float *ybase = a.y + (int64_t)n * a.y_img;
+    auto store_row = [&](int oy) __attribute__((always_inline)) {
+        if (oy < a.OH) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int co = co0 + wq * 16 + 4 * lg + v;
+                if (co >= a.K) continue;
+                float *yrow = ybase + ((int64_t)co * a.OH + oy) * a.OW;
+#pragma unroll
+                for (int f = 0; f < F; ++f) {
+                    const int ox = f * 16 + l16;
+                    if (ox < a.OW) yrow[ox] = acc[f][v];
+                }
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // Rows of this group: r0 + grp + 2t, t < nsteps.  Both groups run every
+    // step (a row past the image computes on zeros and stores nothing), so
+    // the block's barriers stay matched.
+    stage(hs0, r0 + grp);
+    wait_lds_dma();
+    __syncthreads();
+    for (int t = 0; t < nsteps; t += 2) {
+        const int oy = r0 + grp + 2 * t;
+        if (t + 1 < nsteps) stage(hs1, oy + 2);
+        compute(hs0);
+        wait_lds_dma();
+        __syncthreads();
+        store_row(oy);
+        if (t + 1 >= nsteps) break;
+        if (t + 2 < nsteps) stage(hs0, oy + 4);
+        compute(hs1);
+        wait_lds_dma();
+        __syncthreads();
+        store_row(oy + 2);
+    }
+}
+
+}  // namespace katsu

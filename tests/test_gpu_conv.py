@@ -221,3 +221,22 @@ def test_batch_linearity_of_filter_gradient(dev):
     s_oc = xs.max() * gs.sum(axis=(0, 2, 3))
     s = np.broadcast_to(s_oc[:, None, None, None], w.shape)
     assert_within((a + b).cpu().numpy(), full.cpu().numpy(), s, 32 * 56 * 56, "linearity")
+
+
+@pytest.mark.parametrize("xs", [(4, 3, 224, 224), (8, 3, 150, 130), (3, 2, 101, 99)])
+def test_stem_forward_direct(xs, dev):
+    """7x7 stride-2 forward with few input channels (stem-like layers at
+    sizes between the small cases and the full config-5 sampled test), full
+    output against the oracle; (3,2,101,99) has two channels and odd
+    sizes."""
+    import torch
+
+    from katsu_amd import ops
+    ws = (64, xs[1], 7, 7)
+    x = synth.uniform(301, xs)
+    w = synth.normal(302, ws)
+    y = ops.conv2d_forward(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), 2, 3)
+    torch.cuda.synchronize()
+    y_ref = O.conv2d_forward(x, w, 2, 3)
+    ys = O.conv2d_forward(np.abs(x), np.abs(w), 2, 3)
+    assert_within(y.cpu().numpy(), y_ref, ys, xs[1] * 49, f"stem fwd {xs}")
