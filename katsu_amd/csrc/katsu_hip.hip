@@ -1164,12 +1164,78 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
 // ---------------------------------------------------------------------------
 // Backward filter.
 
+// The stem's filter gradient (stem_dw_kernel): 3 channels, 7x7, stride 2.
+struct StemDwPlan {
+    bool ok = false;
+    StemDwArgs a;
+    int64_t blocks = 0;
+    int splits = 0;
+    size_t ws_bytes = 0;
+};
+
+StemDwPlan stem_dw_plan(const ConvDims &d) {
+    StemDwPlan pl;
+    using Geo = StemDwGeo<3, 7, 7>;
+    if (d.C != 3 || d.R != 7 || d.S != 7 || d.st != 2) return pl;
+    if ((int64_t)d.CHW * 4 >= (int64_t)kMaxBufBytes ||
+        (int64_t)d.KOHW * 4 >= (int64_t)kMaxBufBytes)
+        return pl;
+    const int64_t tiles_row = cdiv(d.OW, Geo::TW);
+    const int64_t tiles_total = (int64_t)d.N * d.OH * tiles_row;
+    if (tiles_total > kI32Max) return pl;
+    const int64_t co_blocks = cdiv(d.K, 64);
+    // About one block per CU, each with an even share of the tiles.
+    int64_t splits = std::max<int64_t>(1, kMinDirectBlocks / co_blocks);
+    int64_t tpb = cdiv(tiles_total, splits);
+    tpb += tpb & 1;
+    splits = cdiv(tiles_total, tpb);
+    StemDwArgs &a = pl.a;
+    a.x = nullptr;
+    a.g = nullptr;
+    a.part = nullptr;
+    a.N = d.N;
+    a.C = d.C;
+    a.H = d.H;
+    a.W = d.W;
+    a.K = d.K;
+    a.OH = d.OH;
+    a.OW = d.OW;
+    a.pad = d.pad;
+    a.x_img = d.CHW;
+    a.g_img = d.KOHW;
+    a.tiles_row = (int)tiles_row;
+    a.tiles_total = (int)tiles_total;
+    a.tiles_per_block = (int)tpb;
+    a.co_blocks = (int)co_blocks;
+    a.pstride = ((int64_t)d.K * d.CRS + 3) / 4 * 4;
+    pl.ok = true;
+    pl.splits = (int)splits;
+    pl.blocks = co_blocks * splits;
+    pl.ws_bytes = (size_t)splits * (size_t)a.pstride * sizeof(float);
+    return pl;
+}
+
+int stem_dw_launch(StemDwPlan pl, const float *x, const float *gy, float *dw, float beta,
+                   float *ws, hipStream_t st) {
+    using Geo = StemDwGeo<3, 7, 7>;
+    pl.a.x = x;
+    pl.a.g = gy;
+    pl.a.part = ws;
+    constexpr auto kern = stem_dw_kernel<3, 7, 7, 2>;
+    int rc = lds_optin<kern>(Geo::kBytes);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3((unsigned)pl.blocks), dim3(512), Geo::kBytes, st>>>(pl.a);
+    if ((rc = launch_status()) != KATSU_OK) return rc;
+    return launch_split_reduce(ws, dw, (int64_t)pl.a.K * 147, pl.a.pstride, pl.splits, beta, st);
+}
+
 struct DwPlan {
     int tiles_m, tiles_n, splits, kchunk;
     int64_t pstride;  // floats between partials (a multiple of 4)
     size_t ws_bytes;
     DirectDwPlan direct;  // used when direct.ok
     PwDwPlan pw;          // used when pw.ok (1x1, no padding)
+    StemDwPlan stem;      // used when stem.ok
 };
 
 template <class C>
@@ -1207,6 +1273,13 @@ DwPlan dw_plan_any(const ConvDims &d) {
         DwPlan pl{};
         pl.ws_bytes = pp.ws_bytes;
         pl.pw = pp;
+        return pl;
+    }
+    const StemDwPlan sp = stem_dw_plan(d);
+    if (sp.ok) {
+        DwPlan pl{};
+        pl.ws_bytes = sp.ws_bytes;
+        pl.stem = sp;
         return pl;
     }
     return dw_plan<CfgW>(d);
@@ -1280,6 +1353,7 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     }
     if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
     if (pl.pw.ok) return pw_dw(x, gy, dw, d, pl.pw, beta, wsp, st);
+    if (pl.stem.ok) return stem_dw_launch(pl.stem, x, gy, dw, beta, wsp, st);
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 

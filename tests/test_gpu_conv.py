@@ -240,3 +240,25 @@ def test_stem_forward_direct(xs, dev):
     y_ref = O.conv2d_forward(x, w, 2, 3)
     ys = O.conv2d_forward(np.abs(x), np.abs(w), 2, 3)
     assert_within(y.cpu().numpy(), y_ref, ys, xs[1] * 49, f"stem fwd {xs}")
+
+
+@pytest.mark.parametrize("xs", [(4, 3, 224, 224), (5, 3, 61, 150), (1, 3, 20, 300)])
+def test_stem_filter_gradient(xs, dev):
+    """7x7 stride-2 filter gradient of a 3-channel layer (the stem kernel:
+    56-pixel half-row tiles, two row groups per block, one partial per block)
+    against the oracle.  (5,3,61,150) has 75-pixel rows, so its second tile
+    of each row is partly empty; (1,3,20,300) has 150-pixel rows (three
+    tiles, the last partial) and few tiles per block."""
+    import torch
+
+    from katsu_amd import ops
+    ws = (64, 3, 7, 7)
+    x = synth.uniform(311, xs)
+    oh, ow = (xs[2] + 6 - 7) // 2 + 1, (xs[3] + 6 - 7) // 2 + 1
+    g = synth.normal(313, (xs[0], 64, oh, ow))
+    dw = ops.conv2d_backward_filter(torch.from_numpy(x).to(dev), torch.from_numpy(g).to(dev),
+                                    ws, 2, 3)
+    torch.cuda.synchronize()
+    _, dw_ref = O.conv2d_backward(x, np.zeros(ws, np.float32), g, 2, 3)
+    _, dws = O.conv2d_backward(np.abs(x), np.zeros(ws, np.float32), np.abs(g), 2, 3)
+    assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, f"stem dW {xs}")
