@@ -1184,10 +1184,9 @@ StemDwPlan stem_dw_plan(const ConvDims &d) {
     const int64_t tiles_total = (int64_t)d.N * d.OH * tiles_row;
     if (tiles_total > kI32Max) return pl;
     const int64_t co_blocks = cdiv(d.K, 64);
-    // About one block per CU, each with an even share of the tiles.
-    int64_t splits = std::max<int64_t>(1, kMinDirectBlocks / co_blocks);
-    int64_t tpb = cdiv(tiles_total, splits);
-    tpb += tpb & 1;
+    // About two blocks per CU, each with an equal share of the tiles.
+    int64_t splits = std::max<int64_t>(1, 2 * kMinDirectBlocks / co_blocks);
+    const int64_t tpb = cdiv(tiles_total, splits);
     splits = cdiv(tiles_total, tpb);
     StemDwArgs &a = pl.a;
     a.x = nullptr;
@@ -1224,7 +1223,7 @@ int stem_dw_launch(StemDwPlan pl, const float *x, const float *gy, float *dw, fl
     constexpr auto kern = stem_dw_kernel<3, 7, 7, 2>;
     int rc = lds_optin<kern>(Geo::kBytes);
     if (rc != KATSU_OK) return rc;
-    kern<<<dim3((unsigned)pl.blocks), dim3(512), Geo::kBytes, st>>>(pl.a);
+    kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
     if ((rc = launch_status()) != KATSU_OK) return rc;
     return launch_split_reduce(ws, dw, (int64_t)pl.a.K * 147, pl.a.pstride, pl.splits, beta, st);
 }

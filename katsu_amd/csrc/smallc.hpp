@@ -219,17 +219,17 @@ namespace katsu {
 // GEMM view: i = o (64 per block), j = (c, r, s) in the filter's own order
 // (C*R*S = 147 columns, padded to 160), k = output pixel.  A tile is 56
 // output pixels of one row (TW); a k-step takes four of them, lane group lg
-// taking pixel 4t + lg.  Wave (wm, wn) of a group owns channels 32wm..32wm+31
-// and columns 80wn..80wn+79: 2 A and 5 B fragments, 10 MFMAs per k-step.
-// A lane's B address is a per-lane base (its column's (c, r, s) offset in the
+// taking pixel 4t + lg.  Wave (wm, wn) owns channels 32wm..32wm+31 and
+// columns 80wn..80wn+79: 2 A and 5 B fragments, 10 MFMAs per k-step.  A
+// lane's B address is a per-lane base (its column's (c, r, s) offset in the
 // halo plus lg*ST) plus 4t*ST; its A address a per-lane base plus 4t.
 //
-// Blocks are 512 threads as in the forward: two groups walk alternate tiles
-// of the block's range through double-buffered stages of G (64 rows of 56,
-// pitch 58) and the x halo (3 channels x 7 rows of 128 columns, pitch 136),
-// all staged by LDS-direct loads.  At the end group 1 hands its sums to
-// group 0 through LDS (a fixed order) and the block writes one partial
-// dw[o][c*R*S] slice; the slices are summed by dw_split_reduce.
+// A block (four waves, two per CU) walks a contiguous range of tiles
+// through double-buffered stages of G (64 rows of 56, pitch 58) and the x
+// halo (3 channels x 7 rows of 128 columns, pitch 136), all staged by
+// LDS-direct loads, and writes one partial dw[o][c*R*S] slice; the slices
+// are summed by dw_split_reduce in a fixed order.  The blocks sharing a CU
+// run out of phase, so one's staging overlaps the other's MFMAs.
 struct StemDwArgs {
     const float *x, *g;
     float *part;          // partial slices [split][K][C*R*S], pitch pstride
@@ -251,26 +251,22 @@ struct StemDwGeo {
     static constexpr int CPX = R * XP;          // halo channel pitch
     static constexpr int XS = CC * CPX;         // halo stage
     static constexpr int STAGE = GS + XS;
-    static constexpr int TOTAL = 4 * STAGE;     // two groups x two stages
-    static constexpr size_t kBytes = (size_t)TOTAL * sizeof(float);
+    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
     static constexpr int NCOL = CC * R * S;     // filter columns
     static_assert(NCOL <= 160, "five 16-column fragments per wave half");
-    static_assert(4 * 64 * 40 <= TOTAL, "group hand-off fits in the stages");
 };
 
 template <int CC, int R, int S, int ST>
-__global__ void __launch_bounds__(512, 1) stem_dw_kernel(const StemDwArgs a) {
+__global__ void __launch_bounds__(256, 2) stem_dw_kernel(const StemDwArgs a) {
     using Geo = StemDwGeo<CC, R, S>;
     constexpr int TW = Geo::TW;
     constexpr int NT = TW / 4;  // k-steps per tile
     static_assert((TW - 1) * ST + S <= 128, "halo columns of a tile fit the staged 128");
 
     extern __shared__ float smem[];
-    const int tid = threadIdx.x;
-    const int grp = tid >> 8, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int l16 = lane & 15, lg = lane >> 4;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wq = wv & 3, wm = wq & 1, wn = wq >> 1;
+    const int wq = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wq & 1, wn = wq >> 1;
 
     const int b = blockIdx.x;
     const int cb = b % a.co_blocks;
@@ -278,41 +274,59 @@ __global__ void __launch_bounds__(512, 1) stem_dw_kernel(const StemDwArgs a) {
     const int co0 = cb * 64;
     const int tb = split * a.tiles_per_block;
     const int te = min(tb + a.tiles_per_block, a.tiles_total);
-    const int nsteps = (te - tb + 1) / 2;  // tiles per group (the last may be empty)
 
-    float *st0 = smem + grp * 2 * Geo::STAGE;
-    float *st1 = st0 + Geo::STAGE;
+    float *st0 = smem;
+    float *st1 = smem + Geo::STAGE;
 
-    // Staging of tile `tile` (empty past te): G rows o of pixels [x0, x0+56)
-    // of row oy; halo rows oy*ST - pad + r, columns x0*ST - pad + col, col < 128.
-    auto stage = [&](float *stg, int tile) __attribute__((always_inline)) {
-        const bool tok = tile < te;
-        const int tt = tok ? tile : tb;
-        const int rowi = tt / a.tiles_row;
-        const int n = rowi / a.OH, oy = rowi - (rowi / a.OH) * a.OH;
-        const int x0 = (tt - rowi * a.tiles_row) * TW;
+    // Tile coordinates, advanced one tile at a time: image n, row oy,
+    // first pixel x0 of the row.
+    struct Pos { int n, oy, x0; };
+    auto advance = [&](Pos p) __attribute__((always_inline)) {
+        p.x0 += TW;
+        if (p.x0 >= a.tiles_row * TW) {
+            p.x0 = 0;
+            if (++p.oy == a.OH) {
+                p.oy = 0;
+                ++p.n;
+            }
+        }
+        return p;
+    };
+    Pos p0;
+    {
+        const int rowi = tb / a.tiles_row;
+        p0.n = rowi / a.OH;
+        p0.oy = rowi - p0.n * a.OH;
+        p0.x0 = (tb - rowi * a.tiles_row) * TW;
+    }
+
+    // Staging of the tile at p (nothing but zeros when ok is false): G rows
+    // o of pixels [x0, x0+56) of row oy; halo rows oy*ST - pad + r, columns
+    // x0*ST - pad + col, col < 128.
+    auto stage = [&](float *stg, const Pos &p, bool tok) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t rg =
-            buf_rsrc(a.g + (int64_t)n * a.g_img, (uint32_t)(a.g_img * 4));
+            buf_rsrc(a.g + (int64_t)p.n * a.g_img, (uint32_t)(a.g_img * 4));
         const __amdgpu_buffer_rsrc_t rx =
-            buf_rsrc(a.x + (int64_t)n * a.x_img, (uint32_t)(a.x_img * 4));
-        // G: 64 rows, 16 per wave of the group; lanes past the 56 columns idle.
-        const int px = x0 + lane;
-        const bool pok = tok && lane < TW && px < a.OW;
+            buf_rsrc(a.x + (int64_t)p.n * a.x_img, (uint32_t)(a.x_img * 4));
+        // G: 16 rows per wave; lanes past the 56 columns idle.
+        const int px = p.x0 + lane;
+        const bool pok = tok && px < a.OW;
+        const int gb = (co0 * a.OH + p.oy) * a.OW + px;
+        const int gstep = a.OH * a.OW;
         if (lane < TW) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int o = wq * 16 + i;
                 const bool ok = pok && co0 + o < a.K;
-                lds_dma_b32(rg, stg + o * Geo::GP,
-                            ok ? (((co0 + o) * a.OH + oy) * a.OW + px) * 4 : kOOB);
+                lds_dma_b32(rg, stg + o * Geo::GP, ok ? (gb + o * gstep) * 4 : kOOB);
             }
         }
         // Halo: wave q stages column chunk q & 1 of the (c, r) rows with
         // index parity q >> 1.
         const int col = (wq & 1) * 64 + lane;
-        const int ix = x0 * ST - a.pad + col;
+        const int ix = p.x0 * ST - a.pad + col;
         const int colb = (tok && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
-        const int iy0 = oy * ST - a.pad;
+        const int iy0 = p.oy * ST - a.pad;
         float *xs = stg + Geo::GS + (wq & 1) * 64;
 #pragma unroll
         for (int i = 0; i < CC * R; ++i) {
@@ -320,6 +334,7 @@ __global__ void __launch_bounds__(512, 1) stem_dw_kernel(const StemDwArgs a) {
             const int c = i / R, r = i - (i / R) * R;
             const int iy = iy0 + r;
             const bool ok = (unsigned)iy < (unsigned)a.H;
+            // colb may be kOOB: kOOB plus a row offset (< 1 GiB) stays out of range.
             lds_dma_b32(rx, xs + c * Geo::CPX + r * Geo::XP,
                         ok ? (c * a.H + iy) * a.W * 4 + colb : kOOB);
         }
@@ -373,37 +388,28 @@ __global__ void __launch_bounds__(512, 1) stem_dw_kernel(const StemDwArgs a) {
         }
     };
 
-    // Tiles tb + grp + 2i, i < nsteps, for both groups (matched barriers).
-    stage(st0, tb + grp);
-    wait_lds_dma();
-    __syncthreads();
-    for (int i = 0; i < nsteps; i += 2) {
-        const int tile = tb + grp + 2 * i;
-        if (i + 1 < nsteps) stage(st1, tile + 2);
-        compute(st0);
+    if (tb < te) {
+        Pos cur = p0;
+        stage(st0, cur, true);
         wait_lds_dma();
         __syncthreads();
-        if (i + 1 >= nsteps) break;
-        if (i + 2 < nsteps) stage(st0, tile + 4);
-        compute(st1);
-        wait_lds_dma();
-        __syncthreads();
+        for (int tile = tb; tile < te; tile += 2) {
+            Pos nxt = advance(cur);
+            if (tile + 1 < te) stage(st1, nxt, true);
+            compute(st0);
+            wait_lds_dma();
+            __syncthreads();
+            if (tile + 1 >= te) break;
+            cur = advance(nxt);
+            if (tile + 2 < te) stage(st0, cur, true);
+            compute(st1);
+            wait_lds_dma();
+            __syncthreads();
+        }
     }
 
-    // Group 1's sums to group 0 (value idx of thread t at idx*256 + t), then
-    // group 0 writes the block's partial.
-    float *red = smem;
-    const int t256 = tid & 255;
-    if (grp == 1) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int f = 0; f < 5; ++f)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) red[((i * 5 + f) * 4 + v) * 256 + t256] = acc[i][f][v];
-    }
-    __syncthreads();
-    if (grp == 1) return;
+    // D layout: fragment (i, f), register v is channel wm*32 + 16i + 4lg + v,
+    // column 80wn + 16f + l16.
     float *part = a.part + (int64_t)split * a.pstride;
 #pragma unroll
     for (int f = 0; f < 5; ++f) {
@@ -414,9 +420,7 @@ __global__ void __launch_bounds__(512, 1) stem_dw_kernel(const StemDwArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int o = wm * 32 + i * 16 + 4 * lg + v;
-                if (co0 + o >= a.K) continue;
-                part[(int64_t)(co0 + o) * Geo::NCOL + j] =
-                    acc[i][f][v] + red[((i * 5 + f) * 4 + v) * 256 + t256];
+                if (co0 + o < a.K) part[(int64_t)(co0 + o) * Geo::NCOL + j] = acc[i][f][v];
             }
     }
 }
