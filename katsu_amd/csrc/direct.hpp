@@ -762,7 +762,7 @@ __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
 // are then added in group order.  The summation tree is fixed by (splits,
 // G), so the result is identical on every run.  Partial rows are pstride
 // floats apart (pstride % 4 == 0, so the float4 loads stay aligned).
-template <int G>
+template <int G, int U>
 __global__ void __launch_bounds__(256) dw_split_reduce(const float *__restrict__ part,
                                                        float *__restrict__ dw, int64_t elems,
                                                        int64_t pstride, int splits, float beta) {
@@ -772,8 +772,7 @@ __global__ void __launch_bounds__(256) dw_split_reduce(const float *__restrict__
     const int64_t e = ((int64_t)blockIdx.x * E4 + col) * 4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (e + 3 < elems) {
-        // Eight loads in flight per thread, then added in split order.
-        constexpr int U = 8;
+        // U loads in flight per thread, then added in split order.
         for (int k0 = grp; k0 < splits; k0 += U * G) {
             float4 v[U];
 #pragma unroll

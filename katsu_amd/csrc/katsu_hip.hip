@@ -625,12 +625,13 @@ struct DirectDwPlan {
 };
 
 // Fixed-order sum of split-K partials into dw.  G split groups per float4
-// column: the smallest power of two in [8, 64] that keeps each thread's
-// chain at 8 loads or fewer, so the partials stream with many loads in flight.
-template <int G>
+// column, U loads in flight per thread: the smallest G in {8, 16, 32} that
+// keeps each thread's chain at 8 loads, else G = 32 with 16 in flight (a
+// wave then still reads whole 128-byte runs of eight partials).
+template <int G, int U>
 int split_reduce_g(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
                    float beta, hipStream_t st) {
-    dw_split_reduce<G><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
+    dw_split_reduce<G, U><<<dim3((unsigned)cdiv(elems, (256 / G) * 4)), dim3(256), 0, st>>>(
         ws, dw, elems, pstride, splits, beta);
     return launch_status();
 }
@@ -638,10 +639,10 @@ int split_reduce_g(const float *ws, float *dw, int64_t elems, int64_t pstride, i
 int launch_split_reduce(const float *ws, float *dw, int64_t elems, int64_t pstride, int splits,
                         float beta, hipStream_t st) {
     const int64_t chain = cdiv(splits, 8);
-    if (chain <= 8) return split_reduce_g<8>(ws, dw, elems, pstride, splits, beta, st);
-    if (chain <= 16) return split_reduce_g<16>(ws, dw, elems, pstride, splits, beta, st);
-    if (chain <= 32) return split_reduce_g<32>(ws, dw, elems, pstride, splits, beta, st);
-    return split_reduce_g<64>(ws, dw, elems, pstride, splits, beta, st);
+    if (chain <= 8) return split_reduce_g<8, 8>(ws, dw, elems, pstride, splits, beta, st);
+    if (chain <= 16) return split_reduce_g<16, 8>(ws, dw, elems, pstride, splits, beta, st);
+    if (chain <= 32) return split_reduce_g<32, 8>(ws, dw, elems, pstride, splits, beta, st);
+    return split_reduce_g<32, 16>(ws, dw, elems, pstride, splits, beta, st);
 }
 
 template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
