@@ -26,7 +26,7 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-ffp-contract=fast", "-Wall", "-Wno-unused-function",
+    "-ffp-contract=fast-honor-pragmas", "-Wall", "-Wno-unused-function",
 ]
 
 SOURCES = [os.path.join(CSRC, "katsu_hip.hip")]

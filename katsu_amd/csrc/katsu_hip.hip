@@ -23,6 +23,7 @@
 #include "gemm.hpp"
 #include "pointwise.hpp"
 #include "smallc.hpp"
+#include "tiny.hpp"
 
 namespace katsu {
 namespace {
@@ -1019,6 +1020,111 @@ bool stem_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipSt
 }
 
 // ---------------------------------------------------------------------------
+// Few-channel layers on the vector ALUs (tiny.hpp).
+
+// Output-channel bucket of the forward, and the row kernels' LDS: the
+// transposed filter plus the forward's input rows, or dX's G rows.
+int tiny_kb(const ConvDims &d) { return d.K <= 4 ? 4 : d.K <= 8 ? 8 : 16; }
+int64_t tiny_xw(const ConvDims &d) { return (int64_t)(d.OW - 1) * d.st + d.S; }
+int64_t tiny_fwd_lds(const ConvDims &d) {
+    return (((int64_t)d.CRS * tiny_kb(d) + 3) / 4 * 4 + (int64_t)d.C * d.R * tiny_xw(d)) * 4;
+}
+int64_t tiny_dx_lds(const ConvDims &d) {
+    return ((int64_t)d.K * d.RS * 4 + (int64_t)d.K * d.R * d.OW) * 4;
+}
+
+bool tiny_ok(const ConvDims &d) {
+    return d.C <= kTinyC && d.K <= kTinyK && (int64_t)d.K * d.CRS <= kTinyW && d.S <= 8 &&
+           d.R <= 32 &&
+           tiny_fwd_lds(d) <= 65536 && tiny_dx_lds(d) <= 65536 &&
+           (int64_t)d.N * std::max(d.OH, d.H) <= kI32Max;
+}
+
+TinyArgs tiny_args(const ConvDims &d) {
+    TinyArgs a{};
+    a.N = d.N;
+    a.C = d.C;
+    a.H = d.H;
+    a.W = d.W;
+    a.K = d.K;
+    a.R = d.R;
+    a.S = d.S;
+    a.OH = d.OH;
+    a.OW = d.OW;
+    a.st = d.st;
+    a.pad = d.pad;
+    return a;
+}
+
+int tiny_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
+    TinyArgs a = tiny_args(d);
+    a.x = x;
+    a.w = w;
+    a.out = y;
+    a.xw = (int)tiny_xw(d);
+    const dim3 grid((unsigned)((int64_t)d.N * d.OH));
+    const size_t lds = (size_t)tiny_fwd_lds(d);
+    switch (tiny_kb(d)) {
+        case 4: tiny_fwd_kernel<4><<<grid, dim3(256), lds, st>>>(a, w); break;
+        case 8: tiny_fwd_kernel<8><<<grid, dim3(256), lds, st>>>(a, w); break;
+        default: tiny_fwd_kernel<16><<<grid, dim3(256), lds, st>>>(a, w); break;
+    }
+    return launch_status();
+}
+
+int tiny_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float beta,
+            hipStream_t st) {
+    TinyArgs a = tiny_args(d);
+    a.g = gy;
+    a.w = w;
+    a.out = dx;
+    a.beta = beta;
+    tiny_dx_kernel<<<dim3((unsigned)((int64_t)d.N * d.H)), dim3(256), (size_t)tiny_dx_lds(d),
+                     st>>>(a, w);
+    return launch_status();
+}
+
+// dW: one partial per block of output rows, about one block per CU.
+struct TinyDwPlan {
+    bool ok = false;
+    int64_t blocks = 0, rows_per_block = 0, pstride = 0, xw = 0;
+    size_t lds = 0, ws_bytes = 0;
+};
+
+TinyDwPlan tiny_dw_plan(const ConvDims &d) {
+    TinyDwPlan pl;
+    if (!tiny_ok(d)) return pl;
+    const int64_t rows = (int64_t)d.N * d.OH;
+    const int64_t xw = (int64_t)(d.OW - 1) * d.st + d.S;
+    const int64_t lds = ((int64_t)d.K * d.OW + (int64_t)d.C * d.R * xw) * 4;
+    if (rows <= 0 || lds > 65536) return pl;
+    pl.rows_per_block = cdiv(rows, kMinDirectBlocks);
+    pl.blocks = cdiv(rows, pl.rows_per_block);
+    pl.pstride = ((int64_t)d.K * d.CRS + 3) / 4 * 4;
+    pl.xw = xw;
+    pl.lds = (size_t)lds;
+    pl.ws_bytes = (size_t)pl.blocks * (size_t)pl.pstride * sizeof(float);
+    pl.ok = true;
+    return pl;
+}
+
+int tiny_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const TinyDwPlan &pl,
+            float beta, float *ws, hipStream_t st) {
+    TinyArgs a = tiny_args(d);
+    a.x = x;
+    a.g = gy;
+    a.out2 = ws;
+    a.rows_per_block = (int)pl.rows_per_block;
+    a.xw = (int)pl.xw;
+    a.pstride = pl.pstride;
+    tiny_dw_kernel<<<dim3((unsigned)pl.blocks), dim3(256), pl.lds, st>>>(a);
+    const int rc = launch_status();
+    if (rc != KATSU_OK) return rc;
+    return launch_split_reduce(ws, dw, (int64_t)d.K * d.CRS, pl.pstride, (int)pl.blocks, beta,
+                               st);
+}
+
+// ---------------------------------------------------------------------------
 // Forward.
 
 template <class C>
@@ -1063,6 +1169,7 @@ int conv_fwd_dev(const float *x, const float *w, float *y, const katsu_conv_geom
         if (stem_fwd(x, w, y, d, st, &rc)) return rc;
     }
     if (pw_ok(d)) return pw_fwd(x, w, y, d, st);
+    if (tiny_ok(d)) return tiny_fwd(x, w, y, d, st);
     // The largest tile that still gives every CU a block (rows x pixels).
     const int64_t px = d.npix_out;
     if (d.K <= 16) return fwd_cfg<CfgS>(x, w, y, d, st);
@@ -1157,6 +1264,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     if (dx_as_forward(d, gy, w, dx, beta, &P) && direct_fwd<1>(P, st, &rc)) return rc;
     if (dx_superpixel(d, gy, w, dx, beta, st, &rc)) return rc;
     if (pw_ok(d)) return pw_dx(gy, w, dx, d, beta, st);
+    if (tiny_ok(d)) return tiny_dx(gy, w, dx, d, beta, st);
     if (d.C <= 16) return dx_cfg<CfgS>(gy, w, dx, d, beta, st);
     if (d.C <= 64) return dx_cfg<CfgM>(gy, w, dx, d, beta, st);
     return dx_cfg<CfgL>(gy, w, dx, d, beta, st);
@@ -1236,6 +1344,7 @@ struct DwPlan {
     DirectDwPlan direct;  // used when direct.ok
     PwDwPlan pw;          // used when pw.ok (1x1, no padding)
     StemDwPlan stem;      // used when stem.ok
+    TinyDwPlan tiny;      // used when tiny.ok
 };
 
 template <class C>
@@ -1280,6 +1389,13 @@ DwPlan dw_plan_any(const ConvDims &d) {
         DwPlan pl{};
         pl.ws_bytes = sp.ws_bytes;
         pl.stem = sp;
+        return pl;
+    }
+    const TinyDwPlan tp = tiny_dw_plan(d);
+    if (tp.ok) {
+        DwPlan pl{};
+        pl.ws_bytes = tp.ws_bytes;
+        pl.tiny = tp;
         return pl;
     }
     return dw_plan<CfgW>(d);
@@ -1354,6 +1470,7 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
     if (pl.pw.ok) return pw_dw(x, gy, dw, d, pl.pw, beta, wsp, st);
     if (pl.stem.ok) return stem_dw_launch(pl.stem, x, gy, dw, beta, wsp, st);
+    if (pl.tiny.ok) return tiny_dw(x, gy, dw, d, pl.tiny, beta, wsp, st);
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 
@@ -1380,6 +1497,38 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
                        dx_as_forward(d, gy, w, dx, beta, &P) &&
                        P.CO >= FwdV::KT && direct_fwd_plan<KATSU_FWD_VARIANT, 1>(P, &xp) &&
                        (wpl = dw_plan_any(d)).direct.ok && dw_variant_fusable(wpl.direct.variant);
+    if (!fused && dx != dw && d.npix_in > 0 && d.npix_out > 0 && x && w && gy && tiny_ok(d)) {
+        // Few channels: dX rows and dW partials in one launch, then the reduce.
+        const TinyDwPlan tp = tiny_dw_plan(d);
+        if (tp.ok) {
+            float *wsp = (float *)ws;
+            if (!wsp) {
+                if (!fallback) return KATSU_E_INVALID;
+                const int rc = ensure(*fallback, tp.ws_bytes);
+                if (rc != KATSU_OK) return rc;
+                wsp = (float *)fallback->ptr;
+            } else if (ws_bytes < tp.ws_bytes) {
+                return KATSU_E_INVALID;
+            }
+            TinyArgs a = tiny_args(d);
+            a.x = x;
+            a.g = gy;
+            a.out = dx;
+            a.out2 = wsp;
+            a.beta = beta;
+            a.rows_per_block = (int)tp.rows_per_block;
+            a.xw = (int)tp.xw;
+            a.pstride = tp.pstride;
+            const int64_t ndx = (int64_t)d.N * d.H;
+            const size_t lds = std::max((size_t)tiny_dx_lds(d), tp.lds);
+            tiny_bwd_kernel<<<dim3((unsigned)(ndx + tp.blocks)), dim3(256), lds, st>>>(a, w,
+                                                                                      (int)ndx);
+            const int rc = launch_status();
+            if (rc != KATSU_OK) return rc;
+            return launch_split_reduce(wsp, dw, (int64_t)d.K * d.CRS, tp.pstride, (int)tp.blocks,
+                                       beta, st);
+        }
+    }
     if (!fused) {
         const int rc = conv_bwd_data_dev(gy, w, dx, g, beta, st);
         if (rc != KATSU_OK) return rc;

@@ -262,3 +262,41 @@ def test_stem_filter_gradient(xs, dev):
     _, dw_ref = O.conv2d_backward(x, np.zeros(ws, np.float32), g, 2, 3)
     _, dws = O.conv2d_backward(np.abs(x), np.zeros(ws, np.float32), np.abs(g), 2, 3)
     assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, f"stem dW {xs}")
+
+
+@pytest.mark.parametrize("xs,ws,st,p", [
+    ((1, 3, 224, 224), (8, 3, 3, 3), 1, 1),   # config 1 (the repo example's shape)
+    ((2, 2, 9, 11), (5, 2, 3, 2), 2, 1),      # stride 2, rectangular filter
+    ((3, 4, 7, 6), (16, 4, 2, 2), 1, 2),      # padding wider than the filter overhang
+    ((1, 1, 5, 5), (3, 1, 5, 5), 3, 2),
+])
+def test_few_channel_bit_exact(xs, ws, st, p, dev):
+    """Layers with at most 4 input and 16 output channels run on the vector
+    ALUs in the reference's own summation order with separate multiply and
+    add roundings: the forward and dX equal the oracle (the reference's
+    loops) bit for bit; dW is a parallel sum, within the f32 bound.  beta = 1
+    adds dX into an existing buffer with one more rounding, as the engine's
+    pending += does."""
+    import torch
+
+    from katsu_amd import ops
+    x = synth.uniform(321, xs)
+    w = synth.normal(322, ws)
+    oh = (xs[2] + 2 * p - ws[2]) // st + 1
+    ow = (xs[3] + 2 * p - ws[3]) // st + 1
+    g = synth.normal(323, (xs[0], ws[0], oh, ow))
+    xd, wd, gd = (torch.from_numpy(a).to(dev) for a in (x, w, g))
+    y = ops.conv2d_forward(xd, wd, st, p)
+    dx = ops.conv2d_backward_data(gd, wd, xs, st, p)
+    dw = ops.conv2d_backward_filter(xd, gd, ws, st, p)
+    dx0 = synth.uniform(324, xs)
+    dxa = torch.from_numpy(dx0.copy()).to(dev)
+    ops.conv2d_backward_data(gd, wd, xs, st, p, out=dxa, beta=1.0)
+    torch.cuda.synchronize()
+    y_ref = O.conv2d_forward(x, w, st, p)
+    dx_ref, dw_ref = O.conv2d_backward(x, w, g, st, p)
+    assert np.array_equal(y.cpu().numpy(), y_ref), "forward not bit-exact"
+    assert np.array_equal(dx.cpu().numpy(), dx_ref), "dX not bit-exact"
+    assert np.array_equal(dxa.cpu().numpy(), (dx0 + dx_ref).astype(np.float32)), "dX beta=1"
+    _, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
+    assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, "few-channel dW")
