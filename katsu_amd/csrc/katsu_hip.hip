@@ -1035,7 +1035,8 @@ int64_t tiny_dx_lds(const ConvDims &d) {
 
 bool tiny_ok(const ConvDims &d) {
     return d.C <= kTinyC && d.K <= kTinyK && (int64_t)d.K * d.CRS <= kTinyW && d.S <= 8 &&
-           d.R <= 32 &&
+           d.R <= 32 && (int64_t)d.CHW * 4 < (int64_t)kMaxBufBytes &&
+           (int64_t)d.KOHW * 4 < (int64_t)kMaxBufBytes &&
            tiny_fwd_lds(d) <= 65536 && tiny_dx_lds(d) <= 65536 &&
            (int64_t)d.N * std::max(d.OH, d.H) <= kI32Max;
 }

@@ -39,6 +39,20 @@ struct TinyArgs {
 
 constexpr int kTinyC = 4, kTinyK = 16, kTinyW = 256;  // channel limits; filter elements
 
+// Stages `total` floats into dst[0 .. total) with LDS-direct loads, element
+// e from byte offset off(e) of r (kOOB for a zero): every wave load is in
+// flight at once, and the caller waits once (wait_lds_dma) before its barrier.
+template <class Off>
+__device__ __forceinline__ void tiny_stage(__amdgpu_buffer_rsrc_t r, float *dst, int total,
+                                           Off off) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    for (int base = wv * 64; base < total; base += 256) {
+        const int e = base + lane;
+        if (e < total) lds_dma_b32(r, dst + base, off(e));
+    }
+}
+
 
 // Block b computes output row b of the batch (n = b / OH, oy = b % OH): it
 // stages the R input rows under it for every channel (columns
@@ -70,17 +84,15 @@ __global__ void __launch_bounds__(256)
     }
     const int n = blockIdx.x / a.OH, oy = blockIdx.x - (blockIdx.x / a.OH) * a.OH;
     const int iy0 = oy * a.st - a.pad;
-    for (int c = 0; c < a.C; ++c)
-        for (int r = 0; r < a.R; ++r) {
-            const int iy = iy0 + r;
-            const bool rok = (unsigned)iy < (unsigned)a.H;
-            const float *xrow = a.x + (((int64_t)n * a.C + c) * a.H + (rok ? iy : 0)) * a.W;
-            float *dst = xs + (c * a.R + r) * a.xw;
-            for (int col = t; col < a.xw; col += 256) {
-                const int ix = col - a.pad;
-                dst[col] = (rok && (unsigned)ix < (unsigned)a.W) ? xrow[ix] : 0.f;
-            }
-        }
+    const int64_t chw = (int64_t)a.C * a.H * a.W;
+    tiny_stage(buf_rsrc(a.x + n * chw, (uint32_t)(chw * 4)), xs, a.C * a.R * a.xw, [&](int e) {
+        const int cr = e / a.xw, col = e - cr * a.xw;
+        const int c = cr / a.R, iy = iy0 + (cr - c * a.R), ix = col - a.pad;
+        return ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+                   ? ((c * a.H + iy) * a.W + ix) * 4
+                   : kOOB;
+    });
+    wait_lds_dma();
     __syncthreads();
     const int64_t ohw = (int64_t)a.OH * a.OW;
     float *yrow = a.out + (int64_t)n * a.K * ohw + (int64_t)oy * a.OW;
@@ -148,12 +160,15 @@ __device__ __forceinline__ void tiny_dx_block(const TinyArgs &a, const float *__
         const int ty = iy + a.pad - r;
         const bool ok = ty >= 0 && ty % a.st == 0 && ty / a.st < a.OH;
         rmask |= ok ? 1u << r : 0u;
-        for (int k = 0; k < a.K; ++k) {
-            const float *grow = a.g + ((int64_t)n * a.K + k) * ohw + (ok ? (int64_t)(ty / a.st) * a.OW : 0);
-            float *dst = gs + (k * a.R + r) * a.OW;
-            for (int ox = t; ox < a.OW; ox += 256) dst[ox] = ok ? grow[ox] : 0.f;
-        }
     }
+    tiny_stage(buf_rsrc(a.g + n * a.K * ohw, (uint32_t)(a.K * ohw * 4)), gs, a.K * a.R * a.OW,
+               [&](int e) {
+                   const int kr = e / a.OW, ox = e - kr * a.OW;
+                   const int k = kr / a.R, r = kr - k * a.R;
+                   const int ty = iy + a.pad - r;
+                   return (rmask >> r & 1u) ? (int)((k * ohw + (ty / a.st) * a.OW + ox) * 4) : kOOB;
+               });
+    wait_lds_dma();
     __syncthreads();
     const int64_t hw = (int64_t)a.H * a.W;
     float *dxrow = a.out + (int64_t)n * a.C * hw + (int64_t)iy * a.W;
@@ -212,24 +227,25 @@ __device__ __forceinline__ void tiny_dw_block(const TinyArgs &a, float *sm, int 
         k = t / (a.S * a.R * a.C);
     }
     const int64_t ohw = (int64_t)a.OH * a.OW;
+    const int64_t chw = (int64_t)a.C * a.H * a.W;
     float acc = 0.f;
     int n = r0 / a.OH, oy = r0 - n * a.OH;
     for (int row = r0; row < r1; ++row) {
-        const float *gn = a.g + (int64_t)n * a.K * ohw + (int64_t)oy * a.OW;
-        for (int kk = 0; kk < a.K; ++kk)
-            for (int ox = t; ox < a.OW; ox += 256) gs[kk * a.OW + ox] = gn[kk * ohw + ox];
+        tiny_stage(buf_rsrc(a.g + n * a.K * ohw, (uint32_t)(a.K * ohw * 4)), gs, a.K * a.OW,
+                   [&](int e) {
+                       const int kk = e / a.OW, ox = e - kk * a.OW;
+                       return (int)((kk * ohw + (int64_t)oy * a.OW + ox) * 4);
+                   });
         const int iy0 = oy * a.st - a.pad;
-        for (int cc = 0; cc < a.C; ++cc)
-            for (int rr = 0; rr < a.R; ++rr) {
-                const int iy = iy0 + rr;
-                const bool rok = (unsigned)iy < (unsigned)a.H;
-                const float *xrow = a.x + (((int64_t)n * a.C + cc) * a.H + (rok ? iy : 0)) * a.W;
-                float *dst = xs + (cc * a.R + rr) * a.xw;
-                for (int col = t; col < a.xw; col += 256) {
-                    const int ix = col - a.pad;
-                    dst[col] = (rok && (unsigned)ix < (unsigned)a.W) ? xrow[ix] : 0.f;
-                }
-            }
+        tiny_stage(buf_rsrc(a.x + n * chw, (uint32_t)(chw * 4)), xs, a.C * a.R * a.xw,
+                   [&](int e) {
+                       const int cr = e / a.xw, col = e - cr * a.xw;
+                       const int cc = cr / a.R, iy = iy0 + (cr - cc * a.R), ix = col - a.pad;
+                       return ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+                                  ? ((cc * a.H + iy) * a.W + ix) * 4
+                                  : kOOB;
+                   });
+        wait_lds_dma();
         __syncthreads();
         if (t < kcrs) {
             const float *gk = gs + k * a.OW;
