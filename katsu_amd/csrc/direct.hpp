@@ -53,6 +53,9 @@ __device__ __forceinline__ void order_reads_then_mfma() {
 // zero for any byte offset >= the resource size, so `kOOB` (with resources
 // kept below 1 GiB by the host) turns a load into a zero without a branch.
 constexpr int kOOB = 0x40000000;
+#ifndef KATSU_DW_DMA
+#define KATSU_DW_DMA 1
+#endif
 constexpr uint32_t kMaxBufBytes = 0x40000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float *p, uint32_t bytes) {
@@ -604,6 +607,45 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                     xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r / RPL][c];
     };
 
+    // LDS-direct staging of a tile, in the layout store() writes: lane l of
+    // a load lands at +l; G rows take the lanes below gcap only, so a row
+    // never spills into the next (gpitch >= gcap).
+    const int wvu = __builtin_amdgcn_readfirstlane(wave);
+    auto stage_dma = [&](float *base, const TileGeo &tg) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rx =
+            buf_rsrc(a.x + (int64_t)tg.n * a.x_img, (uint32_t)(a.x_img * 4));
+        const __amdgpu_buffer_rsrc_t rg =
+            buf_rsrc(a.g + (int64_t)tg.n * a.g_img, (uint32_t)(a.g_img * 4));
+        const int iy0 = tg.oy0 * a.st - a.pad;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+            const int ci = c0 + wvu + 4 * j;
+#pragma unroll
+            for (int r = 0; r < ROWS; r += RPL) {
+                const int iy = iy0 + r + lrow;
+                const bool rok = ci < a.C && (unsigned)iy < (unsigned)a.H;
+                const int rowb = (ci * a.H + iy) * a.W * 4;
+#pragma unroll
+                for (int c = 0; c < LPR; ++c)
+                    lds_dma_b32(rx, base + gs_floats + (wvu + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
+                                rok ? rowb + colb[c] : kOOB);
+            }
+        }
+        const int p0 = tg.oy0 * a.OW + tg.cx0;
+#pragma unroll
+        for (int i = 0; i < KT / 4; ++i) {
+            const int row = wvu + 4 * i;
+            const int k = k0 + row;
+#pragma unroll
+            for (int c = 0; c < GPC; ++c) {
+                const int px = c * 64 + lane;
+                if (px < a.gcap)
+                    lds_dma_b32(rg, base + row * a.gpitch + c * 64,
+                                (k < a.K && px < tg.np) ? (k * a.OHW + p0 + px) * 4 : kOOB);
+            }
+        }
+    };
+
     floatx4 acc[WKF][RS];
 #pragma unroll
     for (int f = 0; f < WKF; ++f)
@@ -668,6 +710,36 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
             order_reads_then_mfma<WKF + RS, WKF * RS>();
         }
     };
+#if KATSU_DW_DMA
+    if (tb < te) {
+        float *st0 = smem;
+        float *st1 = smem + a.stage;
+        TileGeo cur = geo(tb);
+        stage_dma(st0, cur);
+        wait_lds_dma();
+        __syncthreads();
+        for (int tile = tb; tile < te; tile += 2) {
+            TileGeo nxt = cur;
+            if (tile + 1 < te) {
+                nxt = geo(tile + 1);
+                stage_dma(st1, nxt);
+            }
+            compute(st0, cur);
+            wait_lds_dma();
+            __syncthreads();
+            if (tile + 1 >= te) break;
+            cur = nxt;
+            if (tile + 2 < te) {
+                nxt = geo(tile + 2);
+                stage_dma(st0, nxt);
+            }
+            compute(st1, cur);
+            wait_lds_dma();
+            __syncthreads();
+            cur = nxt;
+        }
+    }
+#else
     if (tb < te) {
         float *st0 = smem;
         float *st1 = smem + a.stage;
@@ -696,6 +768,8 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
             cur = nxt;
         }
     }
+
+#endif
 
     // Epilogue: D[i = oc][j = c] per tap, transposed through LDS into the
     // partial's row order [oc][c][tap], then written as contiguous runs of
