@@ -234,20 +234,61 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         }
     }
 
+    // Per-lane byte offsets of the stage loads for the chunk at ci0 = 0; a
+    // chunk adds a uniform delta.  A kOOB-based offset (< 2^31 with the
+    // image below 1 GiB) stays out of range after the delta.
+    uint32_t in_off[CPW][ROWS / RPL][LPR];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j)
+#pragma unroll
+        for (int r = 0; r < ROWS; r += RPL) {
+            const int iy = iy0 + r + lrow;
+            const bool ok = (unsigned)iy < (unsigned)a.H;
+#pragma unroll
+            for (int c = 0; c < LPR; ++c)
+                in_off[j][r / RPL][c] =
+                    ok ? (uint32_t)(((wv + 4 * j) * a.H + iy) * a.W * 4) + (uint32_t)colb[c]
+                       : (uint32_t)kOOB;
+        }
+    // Weights (WMODE 0, 1): wave load i = 4q + wv of the weight region; the
+    // lane's row and column in it, the offset at ci0 = 0, and whether the row
+    // exists apart from the chunk's channel count.
+    constexpr int WE = WVEC ? 4 : 1;                  // floats per lane per load
+    constexpr int WNI = Geo::WS / (64 * WE);          // wave loads
+    constexpr int WNQ = (WNI + 3) / 4;
+    uint32_t w_off[WMODE == 2 ? 1 : WNQ];
+    int w_col[WMODE == 2 ? 1 : WNQ], w_row[WMODE == 2 ? 1 : WNQ];
+    bool w_ok[WMODE == 2 ? 1 : WNQ];
+    if (WMODE != 2) {
+#pragma unroll
+        for (int q = 0; q < WNQ; ++q) {
+            const int e = ((q * 4 + wv) * 64 + lane) * WE;
+            const int row = e / Geo::WPITCH, col = e - (e / Geo::WPITCH) * Geo::WPITCH;
+            w_row[q] = row;
+            w_col[q] = col;
+            if (WMODE == 0) {
+                const int co = co0 + row;
+                w_ok[q] = row < KT && co < a.CO;
+                w_off[q] = (uint32_t)((co * a.CI * RS + col) * 4);
+            } else {
+                const int lim = min(KT, a.CO - co0) * RS;
+                w_ok[q] = row < CB && col < lim;
+                w_off[q] = (uint32_t)(((row * a.CO + co0) * RS + col) * 4);
+            }
+        }
+    }
+
     auto stage_in = [&](float *stage, int ci0) __attribute__((always_inline)) {
+        const uint32_t din = (uint32_t)ci0 * (uint32_t)(a.H * a.W * 4);
 #pragma unroll
         for (int j = 0; j < CPW; ++j) {
-            const int ci = ci0 + wv + 4 * j;
+            const bool cok = ci0 + wv + 4 * j < a.CI;
 #pragma unroll
-            for (int r = 0; r < ROWS; r += RPL) {
-                const int iy = iy0 + r + lrow;
-                const bool rok = ci < a.CI && (unsigned)iy < (unsigned)a.H;
-                const int rowb = (ci * a.H + iy) * a.W * 4;
+            for (int r = 0; r < ROWS; r += RPL)
 #pragma unroll
                 for (int c = 0; c < LPR; ++c)
                     lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
-                                rok ? rowb + colb[c] : kOOB);
-            }
+                                cok ? (int)(in_off[j][r / RPL][c] + din) : kOOB);
         }
         float *wst = stage + Geo::XS;
         if (WMODE == 2) {
@@ -261,42 +302,20 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             }
             return;
         }
-        // Valid floats of a weight row in this chunk, and its global start.
-        auto woff = [&](int row, int col) __attribute__((always_inline)) {
-            if (WMODE == 0) {
-                const int co = co0 + row;
-                const int lim = min(CB, a.CI - ci0) * RS;
-                return (row < KT && co < a.CO && col < lim) ? ((co * a.CI + ci0) * RS + col) * 4
-                                                            : kOOB;
-            } else {
-                const int ci = ci0 + row;
-                const int lim = min(KT, a.CO - co0) * RS;
-                return (row < CB && ci < a.CI && col < lim) ? ((ci * a.CO + co0) * RS + col) * 4
-                                                            : kOOB;
-            }
-        };
-        if (WVEC) {
-            constexpr int NI = Geo::WS / 256;  // wave loads of 64 float4
-            constexpr int W4P = Geo::WPITCH / 4;
+        // WMODE 0: the chunk's valid columns; WMODE 1: the chunk's channels.
+        const uint32_t dw = WMODE == 0 ? (uint32_t)(ci0 * RS * 4) : (uint32_t)(ci0 * a.CO * RS * 4);
+        const int lim = WMODE == 0 ? min(CB, a.CI - ci0) * RS : 0;
 #pragma unroll
-            for (int q = 0; q < (NI + 3) / 4; ++q) {
-                const int i = q * 4 + wv;
-                if (i < NI) {
-                    const int e4 = i * 64 + lane;
-                    const int row = e4 / W4P, c4 = e4 - (e4 / W4P) * W4P;
-                    lds_dma_b128(rw, wst + i * 256, woff(row, c4 * 4));
-                }
-            }
-        } else {
-            constexpr int NI = Geo::WS / 64;  // wave loads of 64 floats
-#pragma unroll
-            for (int q = 0; q < (NI + 3) / 4; ++q) {
-                const int i = q * 4 + wv;
-                if (i < NI) {
-                    const int e = i * 64 + lane;
-                    const int row = e / Geo::WPITCH, col = e - (e / Geo::WPITCH) * Geo::WPITCH;
-                    lds_dma_b32(rw, wst + i * 64, woff(row, col));
-                }
+        for (int q = 0; q < WNQ; ++q) {
+            const int i = q * 4 + wv;
+            if (i < WNI) {
+                const bool ok = WMODE == 0 ? (w_ok[q] && w_col[q] < lim)
+                                           : (w_ok[q] && ci0 + w_row[q] < a.CI);
+                const int off = ok ? (int)(w_off[q] + dw) : kOOB;
+                if (WVEC)
+                    lds_dma_b128(rw, wst + i * 256, off);
+                else
+                    lds_dma_b32(rw, wst + i * 64, off);
             }
         }
     };
