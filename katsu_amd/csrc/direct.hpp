@@ -12,8 +12,9 @@
 //
 // Global loads go through buffer resources: a lane whose element lies in the
 // padding or past a tensor edge gets an out-of-range offset and reads zero,
-// so staging has no branches.  Weight rows (and G rows in dW) are fetched
-// as 16-byte loads when the host has checked their alignment (WVEC, g_vec).
+// so staging has no branches.  Tiles are staged by LDS-direct loads; weight
+// rows are fetched 16 bytes per lane when the host has checked their
+// alignment (WVEC).
 // Block outputs are transposed through LDS and written as contiguous
 // 16-byte runs.
 //
@@ -53,9 +54,6 @@ __device__ __forceinline__ void order_reads_then_mfma() {
 // zero for any byte offset >= the resource size, so `kOOB` (with resources
 // kept below 1 GiB by the host) turns a load into a zero without a branch.
 constexpr int kOOB = 0x40000000;
-#ifndef KATSU_DW_DMA
-#define KATSU_DW_DMA 1
-#endif
 constexpr uint32_t kMaxBufBytes = 0x40000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float *p, uint32_t bytes) {
@@ -469,7 +467,6 @@ struct DirectDwArgs {
     int gpitch;          // LDS row pitch of the G tile, == 2 (mod 4), >= gcap
     int gcap;            // G floats staged per row: trows*seg_w rounded up to 4
     int stage;           // floats per LDS stage: KT*gpitch + CT*CPITCH
-    int g_vec;           // 1: tile starts and OHW are multiples of 4 (16-byte G rows)
     int out_vec;         // 1: partial rows are 16-byte aligned runs
     int64_t split_stride;  // floats between partials, or 0 when writing dw directly
     float beta;            // applied only when writing dw directly
@@ -502,12 +499,8 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
     constexpr int RS = R * S;
     constexpr int WK = KT / (16 * WKF);  // waves along output channels
     constexpr int CPW = CT / 4;          // input channels staged per wave
-    constexpr int GRW = KT / 4;          // G rows staged per wave (scalar path)
-    constexpr int G4 = 16 * GPC;         // float4 per G tile row, at most
-    constexpr int GQ4 = KT * G4 / 256;   // float4 G loads per thread
     static_assert(KT % (16 * WKF) == 0 && CT % 16 == 0 && WK * (CT / 16) == 4,
                   "4 waves of (16*WKF) x 16 slices");
-    static_assert((KT * G4) % 256 == 0, "G tile must split evenly over the block");
 
     extern __shared__ float smem[];
 
@@ -532,9 +525,6 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
         const int ix = col - a.pad;
         colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
-    float xr[CPW][ROWS / RPL][LPR];
-    float gr[GRW * GPC];  // scalar G path
-    floatx4 gr4[GQ4];     // 16-byte G path
 
     struct TileGeo { int n, oy0, tr, cx0, cx1, np; };
     auto geo = [&](int tile) __attribute__((always_inline)) {
@@ -550,84 +540,9 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
         return tg;
     };
 
-    auto load = [&](const TileGeo &tg) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rx =
-            buf_rsrc(a.x + (int64_t)tg.n * a.x_img, (uint32_t)(a.x_img * 4));
-        const __amdgpu_buffer_rsrc_t rg =
-            buf_rsrc(a.g + (int64_t)tg.n * a.g_img, (uint32_t)(a.g_img * 4));
-        const int iy0 = tg.oy0 * a.st - a.pad;
-#pragma unroll
-        for (int j = 0; j < CPW; ++j) {
-            const int ci = c0 + wave + 4 * j;
-#pragma unroll
-            for (int r = 0; r < ROWS; r += RPL) {
-                const int iy = iy0 + r + lrow;
-                const bool rok = ci < a.C && (unsigned)iy < (unsigned)a.H;
-                const int rowb = (ci * a.H + iy) * a.W * 4;
-#pragma unroll
-                for (int c = 0; c < LPR; ++c)
-                    xr[j][r / RPL][c] = buf_load(rx, rok ? rowb + colb[c] : kOOB);
-            }
-        }
-        // G rows k0..k0+KT of the tile (contiguous pixels from p0).
-        const int p0 = tg.oy0 * a.OW + tg.cx0;
-        if (a.g_vec) {
-#pragma unroll
-            for (int q = 0; q < GQ4; ++q) {
-                const int e4 = q * 256 + tid;
-                const int row = e4 / G4, c4 = e4 % G4;
-                const int k = k0 + row;
-                const bool ok = k < a.K && c4 * 4 < tg.np;
-                gr4[q] = buf_load4(rg, ok ? (k * a.OHW + p0 + c4 * 4) * 4 : kOOB);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < GRW; ++i) {
-                const int k = k0 + wave + 4 * i;
-#pragma unroll
-                for (int c = 0; c < GPC; ++c) {
-                    const int px = c * 64 + lane;
-                    const bool ok = k < a.K && px < tg.np;
-                    gr[i * GPC + c] = buf_load(rg, ok ? (k * a.OHW + p0 + px) * 4 : kOOB);
-                }
-            }
-        }
-    };
-
-    auto store = [&](float *base) __attribute__((always_inline)) {
-        if (a.g_vec) {
-#pragma unroll
-            for (int q = 0; q < GQ4; ++q) {
-                const int e4 = q * 256 + tid;
-                const int row = e4 / G4, c4 = e4 % G4;
-                if (c4 * 4 < a.gcap) {
-                    float *d = base + row * a.gpitch + c4 * 4;  // 8-byte aligned
-                    *reinterpret_cast<float2 *>(d) = make_float2(gr4[q][0], gr4[q][1]);
-                    *reinterpret_cast<float2 *>(d + 2) = make_float2(gr4[q][2], gr4[q][3]);
-                }
-            }
-        } else {
-            float *gs = base + wave * a.gpitch + lane;
-#pragma unroll
-            for (int i = 0; i < GRW; ++i)
-#pragma unroll
-                for (int c = 0; c < GPC; ++c)
-                    if (lane + c * 64 < a.gcap) gs[4 * i * a.gpitch + c * 64] = gr[i * GPC + c];
-        }
-        // Lane l of a load lands at row r + l / PITCH, column l % PITCH
-        // (PITCH 32), or at column c*64 + l: offset r*PITCH + c*64 + l either way.
-        float *xs = base + gs_floats + wave * Geo::CPITCH + lane;
-#pragma unroll
-        for (int j = 0; j < CPW; ++j)
-#pragma unroll
-            for (int r = 0; r < ROWS; r += RPL)
-#pragma unroll
-                for (int c = 0; c < LPR; ++c)
-                    xs[4 * j * Geo::CPITCH + r * Geo::PITCH + c * 64] = xr[j][r / RPL][c];
-    };
-
-    // LDS-direct staging of a tile, in the layout store() writes: lane l of
-    // a load lands at +l; G rows take the lanes below gcap only, so a row
+    // LDS-direct staging of a tile: X halo channel w + 4j of wave w at
+    // (w + 4j)*CPITCH + r*PITCH + c*64 (lane l at +l: a row chunk, or two
+    // 32-float rows); G row k at k*gpitch, lanes below gcap only, so a row
     // never spills into the next (gpitch >= gcap).
     const int wvu = __builtin_amdgcn_readfirstlane(wave);
     auto stage_dma = [&](float *base, const TileGeo &tg) __attribute__((always_inline)) {
@@ -729,7 +644,6 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
             order_reads_then_mfma<WKF + RS, WKF * RS>();
         }
     };
-#if KATSU_DW_DMA
     if (tb < te) {
         float *st0 = smem;
         float *st1 = smem + a.stage;
@@ -758,37 +672,6 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
             cur = nxt;
         }
     }
-#else
-    if (tb < te) {
-        float *st0 = smem;
-        float *st1 = smem + a.stage;
-        TileGeo cur = geo(tb);
-        load(cur);
-        store(st0);
-        __syncthreads();
-        for (int tile = tb; tile < te; tile += 2) {
-            TileGeo nxt = cur;
-            if (tile + 1 < te) {
-                nxt = geo(tile + 1);
-                load(nxt);
-            }
-            compute(st0, cur);
-            if (tile + 1 < te) store(st1);
-            __syncthreads();
-            if (tile + 1 >= te) break;
-            cur = nxt;
-            if (tile + 2 < te) {
-                nxt = geo(tile + 2);
-                load(nxt);
-            }
-            compute(st1, cur);
-            if (tile + 2 < te) store(st0);
-            __syncthreads();
-            cur = nxt;
-        }
-    }
-
-#endif
 
     // Epilogue: D[i = oc][j = c] per tap, transposed through LDS into the
     // partial's row order [oc][c][tap], then written as contiguous runs of

@@ -712,10 +712,6 @@ bool direct_dw_plan(const ConvDims &d, int64_t target_blocks, DirectDwPlan *pl) 
     a.gpitch = (int)gpitch;
     a.gcap = (int)gcap;
     a.stage = (int)stage;
-    // 16-byte G rows need every tile start (a multiple of trows*OW, or of
-    // seg_w within a row) and OHW to be multiples of 4; pointer alignment is
-    // checked at launch.
-    a.g_vec = (d.OHW % 4 == 0 && (trows * d.OW) % 4 == 0 && (segs == 1 || seg_w % 4 == 0)) ? 1 : 0;
     a.out_vec = d.CRS % 4 == 0 ? 1 : 0;
     a.split_stride = 0;
     a.beta = 0.f;
@@ -776,7 +772,6 @@ void dw_bind(DirectDwPlan *pl, const float *x, const float *gy, float *dw, float
     a.out = direct ? dw : ws;
     a.split_stride = direct ? 0 : pl->pstride;
     a.beta = direct ? beta : 0.f;
-    if (!aligned16(gy)) a.g_vec = 0;
     if (!aligned16(a.out)) a.out_vec = 0;
 }
 

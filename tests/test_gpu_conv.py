@@ -300,3 +300,27 @@ def test_few_channel_bit_exact(xs, ws, st, p, dev):
     assert np.array_equal(dxa.cpu().numpy(), (dx0 + dx_ref).astype(np.float32)), "dX beta=1"
     _, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
     assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, "few-channel dW")
+
+
+def test_stem_kernels_two_channel_blocks(dev):
+    """3-channel 7x7 stride-2 layers with 96 output channels: the stem
+    forward and filter-gradient kernels split them into two 64-channel
+    blocks (the second half empty past 96)."""
+    import torch
+
+    from katsu_amd import ops
+    xs, ws = (2, 3, 160, 200), (96, 3, 7, 7)
+    x = synth.uniform(331, xs)
+    w = synth.normal(332, ws)
+    oh, ow = (xs[2] + 6 - 7) // 2 + 1, (xs[3] + 6 - 7) // 2 + 1
+    g = synth.normal(333, (xs[0], ws[0], oh, ow))
+    xd, wd, gd = (torch.from_numpy(a).to(dev) for a in (x, w, g))
+    y = ops.conv2d_forward(xd, wd, 2, 3)
+    dw = ops.conv2d_backward_filter(xd, gd, ws, 2, 3)
+    torch.cuda.synchronize()
+    y_ref = O.conv2d_forward(x, w, 2, 3)
+    ys = O.conv2d_forward(np.abs(x), np.abs(w), 2, 3)
+    assert_within(y.cpu().numpy(), y_ref, ys, 3 * 49, "stem fwd, 96 channels")
+    _, dw_ref = O.conv2d_backward(x, w, g, 2, 3)
+    _, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), 2, 3)
+    assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, "stem dW, 96 channels")
