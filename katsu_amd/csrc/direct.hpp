@@ -82,6 +82,7 @@ __device__ __forceinline__ void lds_dma_b128(__amdgpu_buffer_rsrc_t r, float *ds
 }
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+
 // ---------------------------------------------------------------------------
 // Forward / data-gradient kernel.
 //
@@ -91,7 +92,7 @@ __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0
 // F fragments of 16 pixels each.  Input channels are consumed CB at a time
 // through a two-stage LDS pipeline.
 //
-// Three weight modes (WMODE) make the same kernel serve three problems:
+// Four weight modes (WMODE) make the same kernel serve four problems:
 //   0  forward:  w' = w[CO][CI][R][S] as stored
 //   1  dX, stride 1: in = G, w'[co][ci][r][s] = w[ci][co][R-1-r][S-1-s]
 //   2  dX, stride 2, by super-pixels: in = G, output channel co' = 4c + 2py + px
@@ -101,6 +102,16 @@ __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0
 //      The conv over super-pixels is stride 1 with filter R' x S' and
 //      padding (-amin, -bmin); the epilogue (EPI 1) scatters co' back to
 //      channel c, pixel (2Y+py, 2X+px).
+//   3  dX, stride 2, by phases: in = G, output channel co = c, one
+//      accumulator set per phase (py, px) of super-pixel (Y, X).  Phase
+//      (py, px) at G offset (dy, dx) takes tap r = py + PD - 2dy,
+//      s = px + PD - 2dx of w[k][c][r][s] (stored as in WMODE 1: CB rows of
+//      KT*R*S floats); each G fragment is read once per offset and multiplied
+//      by the weights of every phase that uses the offset, so no MFMA works
+//      on a tap outside the filter, as the mixed-phase rows of WMODE 2 do.
+//      The halo is that of a stride-1 problem over super-pixels with the
+//      offset filter (Dxs2Taps::DR x DS) and padding (-DYMIN, -DXMIN); the
+//      epilogue (EPI 3) writes pixel (2Y+py, 2X+px) of channel c.
 struct DirectArgs {
     const float *in;   // [N][CI][H][W]
     const float *w;    // layer weights (see WMODE)
@@ -121,6 +132,53 @@ struct DirectArgs {
     int g_c, g_r, g_s, g_pad, g_amin, g_bmin, g_crs, fh, fw;
 };
 
+// The (G offset, phase) pairs of the phase-form stride-2 data gradient of an
+// R x S filter with padding PD, ordered by offset.  Along one axis, phase a
+// and tap k meet at G offset d = (a + PD - k) / 2 when a + PD - k is even,
+// so each tap belongs to exactly one (offset, phase) pair: NP = R*S.
+// Lowest (hi = false) or highest G offset along an axis with K taps.
+constexpr int dxs2_bound(int K, int PD, bool hi) {
+    int m = hi ? -(1 << 20) : 1 << 20;
+    for (int a = 0; a < 2; ++a)
+        for (int k = 0; k < K; ++k) {
+            const int e = a + PD - k;
+            if (e % 2 == 0 && (hi ? e / 2 > m : e / 2 < m)) m = e / 2;
+        }
+    return m;
+}
+struct Dxs2Tab {
+    int n;
+    int off[64], ph[64], tap[64];  // offset (dy-DYMIN)*DS + dx-DXMIN, phase 2py+px, tap r*S+s
+};
+constexpr Dxs2Tab dxs2_pairs(int R, int S, int PD) {
+    const int dymin = dxs2_bound(R, PD, false), dxmin = dxs2_bound(S, PD, false);
+    const int ds = dxs2_bound(S, PD, true) - dxmin + 1;
+    const int no = (dxs2_bound(R, PD, true) - dymin + 1) * ds;
+    Dxs2Tab t{};
+    for (int o = 0; o < no; ++o)
+        for (int p = 0; p < 4; ++p) {
+            const int r = (p >> 1) + PD - 2 * (dymin + o / ds);
+            const int c = (p & 1) + PD - 2 * (dxmin + o % ds);
+            if (r >= 0 && r < R && c >= 0 && c < S) {
+                t.off[t.n] = o;
+                t.ph[t.n] = p;
+                t.tap[t.n] = r * S + c;
+                ++t.n;
+            }
+        }
+    return t;
+}
+template <int R, int S, int PD>
+struct Dxs2Taps {
+    static constexpr int DYMIN = dxs2_bound(R, PD, false), DXMIN = dxs2_bound(S, PD, false);
+    static constexpr int DR = dxs2_bound(R, PD, true) - DYMIN + 1;
+    static constexpr int DS = dxs2_bound(S, PD, true) - DXMIN + 1;
+    static constexpr int NO = DR * DS;  // G offsets
+    static constexpr Dxs2Tab tab = dxs2_pairs(R, S, PD);
+    static constexpr int NP = tab.n;
+    static_assert(NO <= 16 && NP == R * S, "every tap in exactly one (offset, phase) pair");
+};
+
 // LDS layout (floats) of the forward kernel.
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE>
 struct DirectFwdGeo {
@@ -131,19 +189,21 @@ struct DirectFwdGeo {
     static constexpr int XS = CB * CPITCH;              // input tile
     // Weight tile, kept in the global order of its rows:
     //   WMODE 0, 2: KT rows (co) of CB*RS floats, pitch CB*RS + 4
-    //   WMODE 1:    CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
+    //   WMODE 1, 3: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
     // Pitches are multiples of 4 floats so 16-byte DMA lands on row
     // boundaries; the region is a whole number of 256-float wave loads.
-    static constexpr int WROWS = WMODE == 1 ? CB : KT;
-    static constexpr int WLEN = WMODE == 1 ? KT * RS : CB * RS;
-    static constexpr int WPITCH = WMODE == 1 ? WLEN + ((16 - WLEN % 32) + 32) % 32 : WLEN + 4;
+    static constexpr bool WBYCI = WMODE == 1 || WMODE == 3;  // weight rows per input channel
+    static constexpr int WROWS = WBYCI ? CB : KT;
+    static constexpr int WLEN = WBYCI ? KT * RS : CB * RS;
+    static constexpr int WPITCH = WBYCI ? WLEN + ((16 - WLEN % 32) + 32) % 32 : WLEN + 4;
     static constexpr int WS = (WROWS * WPITCH + 255) / 256 * 256;
     static_assert(WLEN % 4 == 0 && WPITCH % 4 == 0, "weight rows of whole float4");
     static constexpr int STAGE = XS + WS;
     // Output transpose buffer (reuses the stages after the last chunk).
     static constexpr int TPMAX = (4 / (KT / 16)) * F * 16;  // pixels per tile, at most
     static constexpr int YPITCH = TPMAX + 4;
-    static_assert(KT * YPITCH <= 2 * STAGE, "output tile must fit the LDS stages");
+    static constexpr int NPH = WMODE == 3 ? 4 : 1;  // accumulator sets (phases)
+    static_assert(NPH * KT * YPITCH <= 2 * STAGE, "output tile must fit the LDS stages");
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
     // WMODE 2 weight slots per lane (4-byte wave loads spread over 4 waves).
     static constexpr int WSLOTS = (WS / 64 + 3) / 4;
@@ -151,8 +211,20 @@ struct DirectFwdGeo {
 
 // Block `bid` of `nb` (the kernel below, or the dX half of the fused
 // backward launch).
+//
+// S2 (stride-2 forward): each staged halo row holds its even columns in the
+// first half of the row and its odd columns in the second.  A fragment's 16
+// pixels then read 16 consecutive floats for every tap instead of every
+// other float, which would put two lanes on each LDS bank.
+//
+// RF (row fragments, output rows of at most 16 pixels): fragment f of wave
+// part wpx is output row wpx*F + f of the tile, lane l%16 its column (lanes
+// past the row end repeat the last column and are dropped).  A fragment of
+// 16 consecutive pixels would wrap onto the next row, whose lanes then share
+// LDS banks with the first row's; one row per fragment keeps the 16 lanes on
+// 16 consecutive floats.  Tiles are whole rows.
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool WVEC>
+          bool WVEC, bool S2 = false, bool RF = false, int PD = 0>
 __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     constexpr int RS = R * S;
@@ -163,6 +235,9 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
     static_assert(CB % 4 == 0, "CB must be a multiple of 4");
     static_assert(WMODE != 2 || !WVEC, "gathered weights load 4 bytes per lane");
+    static_assert(!S2 || (WMODE == 0 && PITCH % 2 == 0), "split columns: forward only");
+    static_assert((WMODE == 3) == (EPI == 3), "the phase form has its own epilogue");
+    constexpr int HALF = PITCH / 2;
 
     extern __shared__ float smem[];
 
@@ -183,14 +258,15 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     int pix[F];
 #pragma unroll
     for (int f = 0; f < F; ++f) {
-        int p = p0 + (wpx * F + f) * 16 + (lane & 15);
+        int p = RF ? p0 + (wpx * F + f) * a.OW + min(lane & 15, a.OW - 1)
+                   : p0 + (wpx * F + f) * 16 + (lane & 15);
         p = p < p1 ? p : p0;
         const int oy = a.fd_ow.div(p);
         const int ox = p - oy * a.OW;
-        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * PITCH + ox * a.st;
+        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * PITCH + (S2 ? ox : ox * a.st);
     }
     // Per-lane A-fragment base: row co = woc*16 + l%16, channel l/16.
-    const int abase = WMODE == 1
+    const int abase = Geo::WBYCI
         ? (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS
         : (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS;
 
@@ -207,7 +283,8 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     int colb[LPR];  // byte offset of the lane's column within a row, or kOOB
 #pragma unroll
     for (int c = 0; c < LPR; ++c) {
-        const int col = c * 64 + (PITCH >= 64 ? lane : lane % PITCH);
+        const int q = c * 64 + (PITCH >= 64 ? lane : lane % PITCH);  // LDS position
+        const int col = S2 ? (q < HALF ? 2 * q : 2 * (q - HALF) + 1) : q;
         const int ix = col - a.padx;
         colb[c] = (col < a.ncols && (unsigned)ix < (unsigned)a.W) ? ix * 4 : kOOB;
     }
@@ -330,7 +407,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         const int r = tap / S, s = tap % S;
         const float *ws = base + Geo::XS + abase;
         av = WMODE == 1 ? ws[cs * 4 * Geo::WPITCH + (RS - 1 - tap)] : ws[cs * 4 * RS + tap];
-        const int toff = cs * 4 * Geo::CPITCH + r * PITCH + s;
+        const int toff = cs * 4 * Geo::CPITCH + r * PITCH + (S2 ? (s & 1) * HALF + (s >> 1) : s);
 #pragma unroll
         for (int f = 0; f < F; ++f) b[f] = base[pix[f] + toff];
     };
@@ -339,9 +416,68 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         for (int f = 0; f < F; ++f)
             acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[f], acc[f], 0, 0, 0);
     };
+    // WMODE 3: one accumulator set per phase; acc (above) is phase 0's.
+    floatx4 acc3[WMODE == 3 ? 3 : 1][F];
+#pragma unroll
+    for (int p = 0; p < (WMODE == 3 ? 3 : 1); ++p)
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc3[p][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Micro-step m of a stage = (channel quad m / NP, pair m % NP); the F
+    // G fragments of an offset are read at its first pair into one of two
+    // buffers (alternating by offset), the pair's weight fragment every step.
+    auto compute3 = [&](const float *base) __attribute__((always_inline)) {
+      if constexpr (WMODE == 3) {
+        using Tp = Dxs2Taps<R, S, PD>;
+        constexpr int NP = Tp::NP, NM = (CB / 4) * NP;
+        float bb[2][F];
+        float aa[2];
+        const float *ws = base + Geo::XS + abase;
+        auto fetch_b = [&](int m, float (&b)[F]) __attribute__((always_inline)) {
+            const int cs = m / NP, o = Tp::tab.off[m % NP];
+            const int toff = cs * 4 * Geo::CPITCH + (o / Tp::DS) * PITCH + o % Tp::DS;
+#pragma unroll
+            for (int f = 0; f < F; ++f) b[f] = base[pix[f] + toff];
+        };
+        auto fetch_a = [&](int m, float &av) __attribute__((always_inline)) {
+            av = ws[(m / NP) * 4 * Geo::WPITCH + Tp::tab.tap[m % NP]];
+        };
+        auto gofs = [](int m) { return (m / NP) * Tp::NO + Tp::tab.off[m % NP]; };
+        fetch_b(0, bb[0]);
+        fetch_a(0, aa[0]);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const int g = gofs(m);
+            const bool nb1 = m + 1 < NM && gofs(m + 1) != g;
+            if (m + 1 < NM) {
+                if (nb1) fetch_b(m + 1, bb[(g + 1) & 1]);
+                fetch_a(m + 1, aa[(m + 1) & 1]);
+            }
+            const int ph = Tp::tab.ph[m % NP];
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                if (ph == 0)
+                    acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(aa[m & 1], bb[g & 1][f], acc[f],
+                                                                  0, 0, 0);
+                else
+                    acc3[ph > 0 ? ph - 1 : 0][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        aa[m & 1], bb[g & 1][f], acc3[ph > 0 ? ph - 1 : 0][f], 0, 0, 0);
+            }
+            if (nb1)
+                order_reads_then_mfma<F + 1, F>();
+            else
+                order_reads_then_mfma<1, F>();
+        }
+      }
+    };
+
     // Software pipeline over the k-steps of one stage: the fragments of step
     // kk+1 are read while step kk's MFMAs run.
     auto compute = [&](const float *base) __attribute__((always_inline)) {
+        if (WMODE == 3) {
+            compute3(base);
+            return;
+        }
         constexpr int NK = (CB / 4) * RS;
         float b0[F], b1[F];
         float a0, a1;
@@ -383,17 +519,55 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     // free after the last barrier), then write each output channel's pixel
     // run -- contiguous in NCHW -- as 16-byte stores (EPI 0), or scatter each
     // super-pixel channel to its full-resolution positions (EPI 1).
+    // Phase ph of WMODE 3 takes rows ph*KT .. ph*KT + KT-1 of ys.
     float *ys = smem;
+    auto put = [&](int ph, const floatx4 (&ac)[F]) __attribute__((always_inline)) {
+        float *yp = ys + ph * KT * Geo::YPITCH;
+        if (RF) {
+            // Pixel p0 + row*OW + col sits at ys column row*OW + col.
+            if ((lane & 15) < a.OW) {
 #pragma unroll
-    for (int f = 0; f < F; ++f)
+                for (int f = 0; f < F; ++f)
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            ys[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * 16 + (lane & 15)] =
-                acc[f][v];
+                    for (int v = 0; v < 4; ++v)
+                        yp[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * a.OW +
+                           (lane & 15)] = ac[f][v];
+            }
+        } else {
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    yp[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * 16 +
+                       (lane & 15)] = ac[f][v];
+        }
+    };
+    put(0, acc);
+    if (WMODE == 3) {
+#pragma unroll
+        for (int ph = 1; ph < 4; ++ph) put(ph, acc3[ph > 0 ? ph - 1 : 0]);
+    }
     __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
     const int np = p1 - p0;
-    if (EPI == 1) {
+    if (EPI == 3) {
+        // Element e of a channel's run: super-pixel p0 + e/2, column phase e&1;
+        // consecutive lanes write consecutive pixels of a full-resolution row.
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            float *dst = outb + (int64_t)co * a.fh * a.fw;
+            for (int py = 0; py < 2; ++py)
+                for (int e = lane; e < 2 * np; e += 64) {
+                    const int p = p0 + (e >> 1), px = e & 1;
+                    const int Y = a.fd_ow.div(p);
+                    const int iy = 2 * Y + py, ix = 2 * (p - Y * a.OW) + px;
+                    if (iy < a.fh && ix < a.fw)
+                        store_beta(dst + iy * a.fw + ix,
+                                   ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], a.beta);
+                }
+        }
+    } else if (EPI == 1) {
         for (int row = wave; row < KT; row += 4) {
             const int co = co0 + row;
             if (co >= a.CO) break;
@@ -432,9 +606,10 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
 }
 
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool WVEC>
+          bool WVEC, bool S2 = false, bool RF = false, int PD = 0>
 __global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
-    direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WVEC>(a, blockIdx.x, gridDim.x);
+    direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WVEC, S2, RF, PD>(a, blockIdx.x,
+                                                                               gridDim.x);
 }
 
 // ---------------------------------------------------------------------------

@@ -439,14 +439,21 @@ struct DirectFwdPlan {
     bool wvec = false;
 };
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, bool S2 = false,
+          bool RF = false, int PD = 0>
 bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     if (P.R != R || P.S != S) return false;
+    // Halo filter: the layer's, or for the phase form its G offsets.
+    constexpr int HR = WMODE == 3 ? Dxs2Taps<R, S, PD>::DR : R;
+    constexpr int HS = WMODE == 3 ? Dxs2Taps<R, S, PD>::DS : S;
+    if (RF && P.OW > 16) return false;  // one output row per 16-lane fragment
+    // Split halo rows: every tap's column must stay inside its half row.
+    if (S2 && (P.st != 2 || (P.OW - 1) + (S - 1) / 2 >= PITCH / 2)) return false;
     static_assert(Geo::kBytes <= kLdsMax, "LDS");
     constexpr int WPX = 4 / (KT / 16);
     const int64_t OHW = P.OH * P.OW;
-    const int64_t ncols = (P.OW - 1) * P.st + S;
+    const int64_t ncols = (P.OW - 1) * P.st + HS;
     if (ncols > PITCH) return false;
     // Buffer resources address one image of `in` and all of `w` in bytes.
     const int64_t in_img = P.CI * P.H * P.W;
@@ -456,16 +463,27 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     const int64_t tpmax = (int64_t)WPX * F * 16;
     // The fewest tiles that fit, but enough blocks to fill the chip; tile
     // lengths rounded to whole 16-byte output runs when that still fits.
-    int64_t tiles_img = std::max(cdiv(OHW, tpmax), cdiv(kMinDirectBlocks, co_blocks * P.N));
+    // Row fragments: tiles of whole rows, one row per fragment.
+    const int64_t frag_rows = (int64_t)WPX * F;
+    int64_t tiles_img = RF ? std::max(cdiv(P.OH, frag_rows), cdiv(kMinDirectBlocks, co_blocks * P.N))
+                           : std::max(cdiv(OHW, tpmax), cdiv(kMinDirectBlocks, co_blocks * P.N));
     for (int attempt = 0; attempt < 64; ++attempt, ++tiles_img) {
-        const int64_t even = cdiv(OHW, tiles_img);
-        if (even > tpmax) continue;
-        if (2 * even < tpmax) return false;  // fragments would be under half full
-        // A length rounded to whole 16-byte runs first, else the even split
-        // (which can be whole rows where the rounded one is not).
-        auto rows_of = [&](int64_t px) { return (tile_row_span(px, P.OW, P.OH) - 1) * P.st + R; };
-        int64_t tile_px = (even + 3) / 4 * 4;
-        if (tile_px > tpmax || rows_of(tile_px) > ROWS) tile_px = even;
+        auto rows_of = [&](int64_t px) { return (tile_row_span(px, P.OW, P.OH) - 1) * P.st + HR; };
+        int64_t tile_px;
+        if (RF) {
+            const int64_t rows = cdiv(P.OH, tiles_img);
+            if (rows > frag_rows) continue;
+            if (2 * rows < frag_rows) return false;  // fragments would be under half used
+            tile_px = rows * P.OW;
+        } else {
+            const int64_t even = cdiv(OHW, tiles_img);
+            if (even > tpmax) continue;
+            if (2 * even < tpmax) return false;  // fragments would be under half full
+            // A length rounded to whole 16-byte runs first, else the even split
+            // (which can be whole rows where the rounded one is not).
+            tile_px = (even + 3) / 4 * 4;
+            if (tile_px > tpmax || rows_of(tile_px) > ROWS) tile_px = even;
+        }
         if (rows_of(tile_px) > ROWS) continue;
         const int64_t ntiles = cdiv(OHW, tile_px);
         const int64_t blocks = co_blocks * P.N * ntiles;
@@ -487,7 +505,7 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
         a.OHW = (int)OHW;
         a.HW = (int)(P.H * P.W);
         a.in_img = in_img;
-        a.out_img = WMODE == 2 ? P.g_c * P.fh * P.fw : P.CO * OHW;
+        a.out_img = WMODE >= 2 ? P.g_c * P.fh * P.fw : P.CO * OHW;
         a.tile_px = (int)tile_px;
         a.tiles_img = (int)ntiles;
         a.co_blocks = (int)co_blocks;
@@ -515,17 +533,19 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     return false;
 }
 
-template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI>
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
+          bool S2 = false, bool RF = false, int PD = 0>
 int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
     int rc;
     if (pl.wvec) {
         constexpr auto kern =
-            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WMODE != 2>;
+            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WMODE != 2, S2, RF, PD>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
     } else {
-        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, false>;
+        constexpr auto kern =
+            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, false, S2, RF, PD>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
     }
@@ -534,18 +554,42 @@ int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
 
 // Direct forward-shaped variants: block tile (KT output channels x F
 // fragments per wave), input-channel chunk, filter, halo rows and pitch.
-template <int KT_, int F_, int CB_, int R_, int S_, int ROWS_, int PITCH_>
+template <int KT_, int F_, int CB_, int R_, int S_, int ROWS_, int PITCH_, bool S2_ = false,
+          bool RF_ = false, int PD_ = 0>
 struct FwdVariant {
     static constexpr int KT = KT_, F = F_, CB = CB_, R = R_, S = S_, ROWS = ROWS_, PITCH = PITCH_;
+    static constexpr bool S2 = S2_;  // stride-2 halo rows split by column parity
+    static constexpr bool RF = RF_;  // one output row (<= 16 pixels) per fragment
+    static constexpr int PD = PD_;   // phase form: the layer's padding
 };
 // 3x3 stride 1 (forward and data gradient): 64 x 208-pixel tiles.
 using FwdV = FwdVariant<64, 13, 8, 3, 3, 7, 64>;
-// 3x3 stride 2 forward: 64 x 64-pixel tiles, 32-float halo rows.
-using FwdS2 = FwdVariant<64, 4, 8, 3, 3, 12, 32>;
+// 3x3 stride 2 forward: 64 x 64-pixel tiles, 32-float halo rows split by
+// column parity.
+#ifndef KATSU_FWD_S2_VARIANT
+#define KATSU_FWD_S2_VARIANT 64, 4, 8, 3, 3, 12, 32, true
+#endif
+using FwdS2 = FwdVariant<KATSU_FWD_S2_VARIANT>;
+// 3x3 stride 2 forward on rows of at most 16 pixels: 64 channels x 7 rows,
+// one row per fragment.
+#ifndef KATSU_FWD_S2R_VARIANT
+#define KATSU_FWD_S2R_VARIANT 64, 7, 8, 3, 3, 16, 32, true, true
+#endif
+using FwdS2R = FwdVariant<KATSU_FWD_S2R_VARIANT>;
 // Stride-2 data gradient by super-pixels: a 4x4 super-filter (7x7 layers
 // such as the stem) with few channels, and a 2x2 one (3x3 layers).
 using DxSp4 = FwdVariant<16, 13, 4, 4, 4, 11, 128>;
 using DxSp2 = FwdVariant<64, 7, 16, 2, 2, 8, 32>;
+#ifndef KATSU_DX_SP2R_VARIANT
+#define KATSU_DX_SP2R_VARIANT 64, 7, 16, 2, 2, 8, 32, false, true
+#endif
+using DxSp2R = FwdVariant<KATSU_DX_SP2R_VARIANT>;  // super-pixel rows of at most 16
+// Stride-2 data gradient by phases (WMODE 3), 3x3 filter with padding 1:
+// 16 channels x 8 super-pixel rows of at most 16, 16 G channels per stage.
+#ifndef KATSU_DX_PH_VARIANT
+#define KATSU_DX_PH_VARIANT 16, 2, 16, 3, 3, 8, 32, false, true, 1
+#endif
+using DxPh = FwdVariant<KATSU_DX_PH_VARIANT>;
 
 #define KATSU_FWD_VARIANT FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::PITCH
 
@@ -553,9 +597,11 @@ template <class V, int WMODE, int EPI>
 bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     DirectFwdPlan pl;
     if (P.CO < V::KT / 2 ||
-        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE>(P, &pl))
+        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, V::S2, V::RF,
+                         V::PD>(P, &pl))
         return false;
-    *rc = direct_fwd_run<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, EPI>(pl, st);
+    *rc = direct_fwd_run<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, EPI, V::S2,
+                         V::RF, V::PD>(pl, st);
     return true;
 }
 
@@ -563,8 +609,26 @@ bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
 template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     if (P.st == 1 && P.CO >= FwdV::KT) return try_direct<FwdV, WMODE, 0>(P, st, rc);
-    if (WMODE == 0 && P.st == 2) return try_direct<FwdS2, 0, 0>(P, st, rc);
+    if (WMODE == 0 && P.st == 2) {
+        if (P.OW <= 16 && try_direct<FwdS2R, 0, 0>(P, st, rc)) return true;
+        return try_direct<FwdS2, 0, 0>(P, st, rc);
+    }
     return false;
+}
+
+// The stride-2 data gradient in phase form (direct.hpp, WMODE 3): input G,
+// C output channels over the super-pixel grid, all four phases per block.
+bool dx_phases(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+               hipStream_t st, int *rc) {
+    using Tp = Dxs2Taps<DxPh::R, DxPh::S, DxPh::PD>;
+    if (d.st != 2 || d.R != DxPh::R || d.S != DxPh::S || d.pad != DxPh::PD || d.C < 16)
+        return false;
+    DirectFwdProblem P{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1, -Tp::DYMIN,
+                       -Tp::DXMIN, (d.H + 1) / 2, (d.W + 1) / 2, beta};
+    P.g_c = d.C;
+    P.fh = d.H;
+    P.fw = d.W;
+    return try_direct<DxPh, 3, 3>(P, st, rc);
 }
 
 // The stride-2 data gradient as a stride-1 problem over super-pixels (see
@@ -598,7 +662,10 @@ bool dx_superpixel(const ConvDims &d, const float *gy, const float *w, float *dx
     P.fh = d.H;
     P.fw = d.W;
     if (P.R == DxSp4::R && P.S == DxSp4::S && P.CO <= 16) return try_direct<DxSp4, 2, 1>(P, st, rc);
-    if (P.R == DxSp2::R && P.S == DxSp2::S) return try_direct<DxSp2, 2, 1>(P, st, rc);
+    if (P.R == DxSp2::R && P.S == DxSp2::S) {
+        if (P.OW <= 16 && try_direct<DxSp2R, 2, 1>(P, st, rc)) return true;
+        return try_direct<DxSp2, 2, 1>(P, st, rc);
+    }
     return false;
 }
 
@@ -1258,6 +1325,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     DirectFwdProblem P;
     int rc = KATSU_OK;
     if (dx_as_forward(d, gy, w, dx, beta, &P) && direct_fwd<1>(P, st, &rc)) return rc;
+    if (dx_phases(d, gy, w, dx, beta, st, &rc)) return rc;
     if (dx_superpixel(d, gy, w, dx, beta, st, &rc)) return rc;
     if (pw_ok(d)) return pw_dx(gy, w, dx, d, beta, st);
     if (tiny_ok(d)) return tiny_dx(gy, w, dx, d, beta, st);

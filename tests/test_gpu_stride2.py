@@ -1,15 +1,25 @@
-"""Stride-2 direct kernels against the CPU oracle: the 3x3 stride-2 forward
-(32-float halo rows) and the data gradient by super-pixels (a stride-1
-convolution of G over 2x2 pixel blocks, then scattered back).  Shapes are
-chosen so the planner takes these kernels (enough workgroups to fill the
-GPU), at sizes the oracle finishes in seconds; odd input sizes exercise the
-scatter's edge, where a super-pixel's second row or column lies outside."""
+"""Stride-2 direct kernels against the CPU oracle.
+
+Forward: the 3x3 stride-2 kernel (32-float halo rows split by column
+parity), and on rows of at most 16 output pixels the row-fragment tiles;
+cases cover 14- and 15-pixel rows and input channel counts with and without
+16-byte weight rows.  Data gradient: a 3x3, padding-1 layer with at least 16
+input channels takes the phase form (every MFMA a real tap, all four output
+phases of a channel block in one block); other stride-2 layers take the
+super-pixel form (a stride-1 convolution of G over 2x2 pixel blocks, then
+scattered back).  Phase-form cases cover odd image sizes (a super-pixel's
+second row or column outside the image), channel counts off the 16-channel
+blocks and stages, rows of exactly 16 super-pixels, tiles of 5 rows with a
+short last tile, and beta = 1.  Shapes are chosen so the planner takes these
+kernels (enough workgroups to fill the GPU), at sizes the oracle finishes in
+seconds."""
 import numpy as np
 import pytest
 
 from katsu_amd import synth
 from oracle import oracle as O
 from tests.parity import assert_within, edge_samples, random_samples, sample_dx
+from tests.test_gpu_conv import _check_full
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +49,8 @@ def test_forward_stride2(xs, ws, dev):
 @pytest.mark.parametrize("xs,ws,p", [((32, 64, 28, 28), (128, 64, 3, 3), 1),
                                      ((32, 64, 27, 27), (128, 64, 3, 3), 1),
                                      ((32, 64, 28, 28), (128, 64, 3, 3), 0)])
-def test_data_gradient_superpixel_3x3(xs, ws, p, dev):
+def test_data_gradient_3x3(xs, ws, p, dev):
+    """Padding 1 takes the phase form, padding 0 the super-pixel form."""
     import torch
 
     from katsu_amd import ops
@@ -74,3 +85,62 @@ def test_data_gradient_superpixel_stem(dev):
     pts = random_samples(xs, 2000, 7) + edge_samples(xs)
     ref, sab = sample_dx(g, w, xs, 2, 3, pts)
     assert_within(np.array([dx[t] for t in pts]), ref, sab, 64 * 49, "stem dX")
+
+
+DX_CASES = [
+    ((32, 64, 28, 28), (32, 64, 3, 3)),   # 14 x 14 super-pixels, 7-row tiles
+    ((32, 40, 27, 25), (24, 40, 3, 3)),   # odd sizes; 3 channel blocks; 5-row tiles
+    ((64, 64, 9, 31), (33, 64, 3, 3)),    # 16-wide super rows; a 1-channel last stage
+]
+
+
+@pytest.mark.parametrize("xs,ws", DX_CASES)
+def test_stride2_data_gradient_phases(xs, ws, dev):
+    import torch
+
+    from katsu_amd import ops
+    x = synth.uniform(301, xs)
+    w = synth.uniform(302, ws)
+    oh, ow = (xs[2] - 1) // 2 + 1, (xs[3] - 1) // 2 + 1
+    g = synth.uniform(303, (xs[0], ws[0], oh, ow))
+    wd, gd = torch.from_numpy(w).to(dev), torch.from_numpy(g).to(dev)
+    dx = ops.conv2d_backward_data(gd, wd, xs, 2, 1)
+    torch.cuda.synchronize()
+    dx_ref = O.conv2d_backward_data(xs, w, g, 2, 1)
+    dxs = O.conv2d_backward_data(xs, np.abs(w), np.abs(g), 2, 1)
+    assert_within(dx.cpu().numpy(), dx_ref, dxs, ws[0] * 9, f"{xs}*{ws} dX")
+
+
+def test_stride2_data_gradient_accumulates(dev):
+    """beta = 1 adds the gradient to what dX holds, in every phase."""
+    import torch
+
+    from katsu_amd import ops
+    xs, ws = DX_CASES[1]
+    w = synth.uniform(311, ws)
+    g = synth.uniform(313, (xs[0], ws[0], 14, 13))
+    dx0 = synth.uniform(314, xs)
+    dx = torch.from_numpy(dx0.copy()).to(dev)
+    ops.conv2d_backward_data(torch.from_numpy(g).to(dev), torch.from_numpy(w).to(dev), xs, 2, 1,
+                             out=dx, beta=1.0)
+    torch.cuda.synchronize()
+    dx_ref = O.conv2d_backward_data(xs, w, g, 2, 1)
+    dxs = O.conv2d_backward_data(xs, np.abs(w), np.abs(g), 2, 1)
+    assert_within(dx.cpu().numpy(), dx0.astype(np.float64) + dx_ref, dxs + np.abs(dx0),
+                  ws[0] * 9 + 1, "dX beta=1")
+
+
+FWD_CASES = [
+    ((64, 16, 28, 28), (128, 16, 3, 3)),  # 14-pixel rows, 7-row tiles
+    ((64, 20, 27, 29), (100, 20, 3, 3)),  # 15-pixel rows; a partial channel block
+    ((64, 22, 28, 30), (96, 22, 3, 3)),   # 22 channels: 4-byte weight loads
+]
+
+
+@pytest.mark.parametrize("xs,ws", FWD_CASES)
+def test_stride2_small_image_all_passes(xs, ws, dev):
+    x = synth.uniform(321, xs)
+    w = synth.uniform(322, ws)
+    oh, ow = (xs[2] - 1) // 2 + 1, (xs[3] - 1) // 2 + 1
+    g = synth.uniform(323, (xs[0], ws[0], oh, ow))
+    _check_full(x, w, g, 2, 1, dev, f"{xs}*{ws} s2")
