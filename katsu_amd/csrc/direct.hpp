@@ -48,6 +48,20 @@ __device__ __forceinline__ void order_reads_then_mfma() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
 }
+// The same with nv LDS-direct loads of the next stage issued first (nv is a
+// constant after unrolling, at most 4).
+template <int NREAD, int NMFMA>
+__device__ __forceinline__ void order_step(int nv) {
+    if (nv == 0) {
+        order_reads_then_mfma<NREAD, NMFMA>();
+        return;
+    }
+    if (nv == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM reads
+    if (nv == 2) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    if (nv == 3) __builtin_amdgcn_sched_group_barrier(0x020, 3, 0);
+    if (nv >= 4) __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);
+    order_reads_then_mfma<NREAD, NMFMA>();
+}
 
 // ---------------------------------------------------------------------------
 // Buffer-resource loads.  Range checking of a raw buffer (stride 0) returns
@@ -191,12 +205,14 @@ struct DirectFwdGeo {
     //   WMODE 0, 2: KT rows (co) of CB*RS floats, pitch CB*RS + 4
     //   WMODE 1, 3: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
     // Pitches are multiples of 4 floats so 16-byte DMA lands on row
-    // boundaries; the region is a whole number of 256-float wave loads.
+    // boundaries.  The region is a whole number of 1024 floats, so each of
+    // the 4 waves issues the same number of loads for it (16-byte or 4-byte),
+    // without a per-wave branch; loads past the last row read zeros.
     static constexpr bool WBYCI = WMODE == 1 || WMODE == 3;  // weight rows per input channel
     static constexpr int WROWS = WBYCI ? CB : KT;
     static constexpr int WLEN = WBYCI ? KT * RS : CB * RS;
     static constexpr int WPITCH = WBYCI ? WLEN + ((16 - WLEN % 32) + 32) % 32 : WLEN + 4;
-    static constexpr int WS = (WROWS * WPITCH + 255) / 256 * 256;
+    static constexpr int WS = (WROWS * WPITCH + 1023) / 1024 * 1024;
     static_assert(WLEN % 4 == 0 && WPITCH % 4 == 0, "weight rows of whole float4");
     static constexpr int STAGE = XS + WS;
     // Output transpose buffer (reuses the stages after the last chunk).
@@ -353,46 +369,62 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         }
     }
 
-    auto stage_in = [&](float *stage, int ci0) __attribute__((always_inline)) {
-        const uint32_t din = (uint32_t)ci0 * (uint32_t)(a.H * a.W * 4);
-#pragma unroll
-        for (int j = 0; j < CPW; ++j) {
-            const bool cok = ci0 + wv + 4 * j < a.CI;
-#pragma unroll
-            for (int r = 0; r < ROWS; r += RPL)
-#pragma unroll
-                for (int c = 0; c < LPR; ++c)
-                    lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
-                                cok ? (int)(in_off[j][r / RPL][c] + din) : kOOB);
-        }
-        float *wst = stage + Geo::XS;
-        if (WMODE == 2) {
-            constexpr int NI = Geo::WS / 64;
-#pragma unroll
-            for (int q = 0; q < Geo::WSLOTS; ++q) {
-                const int i = q * 4 + wv;
-                if (i < NI)
-                    lds_dma_b32(rw, wst + i * 64,
-                                wtab[q] >= 0 ? (wtab[q] + ci0 * a.g_crs) * 4 : kOOB);
-            }
+    // Load i of a stage (NSTG per wave): halo loads first, then weight loads.
+    // Issued one or two per k-step inside the previous chunk's MFMA loop
+    // (stage_step), so the wave does not stall on a burst of them at the
+    // chunk boundary.  ci0 >= CI makes every load read zeros, which is how
+    // the last chunk's loop runs.
+    constexpr int NHALO = CPW * (ROWS / RPL) * LPR;
+    constexpr int NWL = WMODE == 2 ? Geo::WS / 256 : Geo::WS / (256 * WE);
+    constexpr int NSTG = NHALO + NWL;
+    static_assert(NSTG <= 4 * (CB / 4) * RS, "at most 4 loads per k-step");
+    static_assert(WMODE == 2 ? (Geo::WS / 64) % 4 == 0 : WNI % 4 == 0, "equal loads per wave");
+    auto stage_part = [&](float *stage, int ci0, int i) __attribute__((always_inline)) {
+        if (i < NHALO) {
+            const int j = i / ((ROWS / RPL) * LPR);
+            const int r = (i / LPR) % (ROWS / RPL) * RPL, c = i % LPR;
+            // A channel past CI gets bit 31 set: out of range (the resource
+            // is below 1 GiB) whatever the sum wraps to.  Computed, not
+            // selected, so the load is not split into branches on the
+            // (uniform) channel test.
+            const uint32_t din = (uint32_t)ci0 * (uint32_t)(a.H * a.W * 4);
+            const uint32_t oob = (uint32_t)(ci0 + wv + 4 * j >= a.CI) << 31;
+            lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
+                        (int)((in_off[j][r / RPL][c] + din) | oob));
             return;
         }
-        // WMODE 0: the chunk's valid columns; WMODE 1: the chunk's channels.
+        const int q = i - NHALO, wi = q * 4 + wv;  // this wave's load q: wave load wi
+        float *wst = stage + Geo::XS;
+        if (WMODE == 2) {
+            lds_dma_b32(rw, wst + wi * 64, wtab[q] >= 0 ? (wtab[q] + ci0 * a.g_crs) * 4 : kOOB);
+            return;
+        }
+        // WMODE 0: the chunk's valid columns; WMODE 1, 3: the chunk's channels.
         const uint32_t dw = WMODE == 0 ? (uint32_t)(ci0 * RS * 4) : (uint32_t)(ci0 * a.CO * RS * 4);
         const int lim = WMODE == 0 ? min(CB, a.CI - ci0) * RS : 0;
+        const bool ok = WMODE == 0 ? (w_ok[q] && w_col[q] < lim)
+                                   : (w_ok[q] && ci0 + w_row[q] < a.CI);
+        const int off = ok ? (int)(w_off[q] + dw) : kOOB;
+        if (WVEC)
+            lds_dma_b128(rw, wst + wi * 256, off);
+        else
+            lds_dma_b32(rw, wst + wi * 64, off);
+    };
+    auto stage_in = [&](float *stage, int ci0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < WNQ; ++q) {
-            const int i = q * 4 + wv;
-            if (i < WNI) {
-                const bool ok = WMODE == 0 ? (w_ok[q] && w_col[q] < lim)
-                                           : (w_ok[q] && ci0 + w_row[q] < a.CI);
-                const int off = ok ? (int)(w_off[q] + dw) : kOOB;
-                if (WVEC)
-                    lds_dma_b128(rw, wst + i * 256, off);
-                else
-                    lds_dma_b32(rw, wst + i * 64, off);
-            }
-        }
+        for (int i = 0; i < NSTG; ++i) stage_part(stage, ci0, i);
+    };
+    // The loads of k-step kk of NK: parts [kk*per, kk*per + per), per the
+    // fewest that finishes them within the loop.
+    auto stage_step = [&](float *stage, int ci0, int kk, int nk) __attribute__((always_inline)) {
+        const int per = (NSTG + nk - 1) / nk;
+#pragma unroll
+        for (int i = kk * per; i < kk * per + per; ++i)
+            if (i < NSTG) stage_part(stage, ci0, i);
+    };
+    auto nsteploads = [](int kk, int nk) {
+        const int per = (NSTG + nk - 1) / nk;
+        return max(0, min(per, NSTG - kk * per));
     };
 
     floatx4 acc[F];
@@ -425,7 +457,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     // Micro-step m of a stage = (channel quad m / NP, pair m % NP); the F
     // G fragments of an offset are read at its first pair into one of two
     // buffers (alternating by offset), the pair's weight fragment every step.
-    auto compute3 = [&](const float *base) __attribute__((always_inline)) {
+    auto compute3 = [&](const float *base, float *nxt, int ci0n) __attribute__((always_inline)) {
       if constexpr (WMODE == 3) {
         using Tp = Dxs2Taps<R, S, PD>;
         constexpr int NP = Tp::NP, NM = (CB / 4) * NP;
@@ -463,19 +495,22 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                     acc3[ph > 0 ? ph - 1 : 0][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                         aa[m & 1], bb[g & 1][f], acc3[ph > 0 ? ph - 1 : 0][f], 0, 0, 0);
             }
+            stage_step(nxt, ci0n, m, NM);
             if (nb1)
-                order_reads_then_mfma<F + 1, F>();
+                order_step<F + 1, F>(nsteploads(m, NM));
             else
-                order_reads_then_mfma<1, F>();
+                order_step<1, F>(nsteploads(m, NM));
         }
       }
     };
 
     // Software pipeline over the k-steps of one stage: the fragments of step
     // kk+1 are read while step kk's MFMAs run.
-    auto compute = [&](const float *base) __attribute__((always_inline)) {
+    // The next chunk's loads go into `nxt` as it runs (ci0n = its first
+    // channel, or CI for none).
+    auto compute = [&](const float *base, float *nxt, int ci0n) __attribute__((always_inline)) {
         if (WMODE == 3) {
-            compute3(base);
+            compute3(base, nxt, ci0n);
             return;
         }
         constexpr int NK = (CB / 4) * RS;
@@ -487,10 +522,14 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         for (int kk = 0; kk < NK; kk += 2) {
             if (kk + 1 < NK) fetch(base, kk + 1, b1, a1);
             mma(b0, a0);
-            order_reads_then_mfma<F + 1, F>();
+            stage_step(nxt, ci0n, kk, NK);
+            order_step<F + 1, F>(nsteploads(kk, NK));
             if (kk + 2 < NK) fetch(base, kk + 2, b0, a0);
-            if (kk + 1 < NK) mma(b1, a1);
-            order_reads_then_mfma<F + 1, F>();
+            if (kk + 1 < NK) {
+                mma(b1, a1);
+                stage_step(nxt, ci0n, kk + 1, NK);
+            }
+            order_step<F + 1, F>(kk + 1 < NK ? nsteploads(kk + 1, NK) : 0);
         }
     };
 
@@ -504,13 +543,11 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     wait_lds_dma();
     __syncthreads();
     for (int ch = 0; ch < nch; ch += 2) {
-        if (ch + 1 < nch) stage_in(st1, (ch + 1) * CB);
-        compute(st0);
+        compute(st0, st1, ch + 1 < nch ? (ch + 1) * CB : a.CI);
         wait_lds_dma();
         __syncthreads();
         if (ch + 1 >= nch) break;
-        if (ch + 2 < nch) stage_in(st0, (ch + 2) * CB);
-        compute(st1);
+        compute(st1, st0, ch + 2 < nch ? (ch + 2) * CB : a.CI);
         wait_lds_dma();
         __syncthreads();
     }
