@@ -144,3 +144,34 @@ def test_stride2_small_image_all_passes(xs, ws, dev):
     oh, ow = (xs[2] - 1) // 2 + 1, (xs[3] - 1) // 2 + 1
     g = synth.uniform(323, (xs[0], ws[0], oh, ow))
     _check_full(x, w, g, 2, 1, dev, f"{xs}*{ws} s2")
+
+
+# 7x7 stride-2 padding-3 data gradient of layers with at most 4 input
+# channels (stem-like), full oracle comparison: odd sizes clip the last
+# super-pixel's second row and column, an odd K, C = 1 and C = 4, beta = 1.
+STEM_DX_CASES = [
+    ((32, 3, 99, 101), (25, 3, 7, 7)),
+    ((64, 4, 64, 72), (16, 4, 7, 7)),
+    ((20, 1, 224, 60), (8, 1, 7, 7)),
+]
+
+
+@pytest.mark.parametrize("xs,ws", STEM_DX_CASES)
+def test_stem_data_gradient(xs, ws, dev):
+    import torch
+
+    from katsu_amd import ops
+    w = synth.uniform(331, ws)
+    oh, ow = (xs[2] - 1) // 2 + 1, (xs[3] - 1) // 2 + 1
+    g = synth.uniform(333, (xs[0], ws[0], oh, ow))
+    wd, gd = torch.from_numpy(w).to(dev), torch.from_numpy(g).to(dev)
+    dx = ops.conv2d_backward_data(gd, wd, xs, 2, 3)
+    dx0 = synth.uniform(334, xs)
+    dx1 = torch.from_numpy(dx0.copy()).to(dev)
+    ops.conv2d_backward_data(gd, wd, xs, 2, 3, out=dx1, beta=1.0)
+    torch.cuda.synchronize()
+    ref = O.conv2d_backward_data(xs, w, g, 2, 3)
+    sab = O.conv2d_backward_data(xs, np.abs(w), np.abs(g), 2, 3)
+    assert_within(dx.cpu().numpy(), ref, sab, ws[0] * 49, f"stem dX {xs}*{ws}")
+    assert_within(dx1.cpu().numpy(), dx0.astype(np.float64) + ref, sab + np.abs(dx0),
+                  ws[0] * 49 + 1, f"stem dX beta=1 {xs}*{ws}")
