@@ -87,6 +87,21 @@ int katsu_hip_gemm_f32(const float *a, const float *b, float *c, size_t m, size_
 int katsu_hip_gemm_f32_dev(const float *a, const float *b, float *c, size_t m, size_t n,
                            size_t k, int trans_a, int trans_b, float beta, void *stream);
 
+/* The whole Matmul VJP on device buffers (Op::backward Matmul arm,
+ * tensor.rs:418-445), for C[m,n] = A[m,k] . B[k,n] with upstream gradient
+ * G[m,n]:
+ *   da[m,k] = beta_a*da + G . B^T     then     db[k,n] = beta_b*db + A^T . G
+ * A NULL da or db skips that product (the parent needs no gradient).  When
+ * da and db overlap (A and B the same node) this is exactly
+ * katsu_hip_gemm_f32_dev(G, B, da, m, k, n, 0, 1, beta_a) followed by
+ * katsu_hip_gemm_f32_dev(A, G, db, k, n, m, 1, 0, beta_b).  Otherwise the
+ * two products may run as one launch, whose k-sums can be added in another
+ * (fixed) order than those two calls': within the same f32 bound, and the
+ * same bits on every call. */
+int katsu_hip_matmul_vjp_f32_dev(const float *a, const float *b, const float *g, float *da,
+                                 float *db, size_t m, size_t k, size_t n, float beta_a,
+                                 float beta_b, void *stream);
+
 /* ---- S3: convolution forward --------------------------------------------
  * y[n,k,oh,ow] = sum over valid (c,r,s) of x[n,c,oy*stride+r-pad,
  * ox*stride+s-pad] * w[k,c,r,s]  (Conv2D::forward, conv2d.rs:95-115;

@@ -15,7 +15,7 @@ OK, E_INVALID, E_NODEVICE, E_OOM, E_LAUNCH = 0, 1, 2, 3, 4
 EXPORTS = (
     "katsu_hip_version", "katsu_hip_strerror", "katsu_hip_init", "katsu_hip_shutdown",
     "katsu_hip_conv2d_geometry",
-    "katsu_hip_gemm_f32", "katsu_hip_gemm_f32_dev",
+    "katsu_hip_gemm_f32", "katsu_hip_gemm_f32_dev", "katsu_hip_matmul_vjp_f32_dev",
     "katsu_hip_conv2d_fwd_f32", "katsu_hip_conv2d_fwd_f32_dev",
     "katsu_hip_conv2d_bwd_data_f32", "katsu_hip_conv2d_bwd_data_f32_dev",
     "katsu_hip_conv2d_bwd_filter_workspace",
@@ -65,6 +65,7 @@ def lib():
         L.katsu_hip_conv2d_geometry.argtypes = [gp]
         L.katsu_hip_gemm_f32.argtypes = [vp, vp, vp, sz, sz, sz, i, i, fp]
         L.katsu_hip_gemm_f32_dev.argtypes = [vp, vp, vp, sz, sz, sz, i, i, fp, vp]
+        L.katsu_hip_matmul_vjp_f32_dev.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, fp, fp, vp]
         L.katsu_hip_conv2d_fwd_f32.argtypes = [vp, vp, vp, gp]
         L.katsu_hip_conv2d_fwd_f32_dev.argtypes = [vp, vp, vp, gp, vp]
         L.katsu_hip_conv2d_bwd_data_f32.argtypes = [vp, vp, vp, gp, fp]

@@ -436,19 +436,22 @@ struct Engine {
             case Op::Kind::Matmul: {
                 // tensor.rs:418-445, seam S2: dA += G.B^T, then dB += A^T.G, into
                 // the pending buffers (the same buffer when A and B are one
-                // node, hence the order).
+                // node: the entry point then runs them in that order, else as
+                // one launch).  dB's beta is read after dA's slot is marked
+                // written, so a shared slot accumulates.
                 const Tensor &a = ps[0], &b = ps[1];
                 const size_t m = a.shape()[0], k = a.shape()[1], n = b.shape()[1];
                 if (node.numel() == 0 || k == 0) break;
                 KATSU_TRY(ad, a.device_data());
                 KATSU_TRY(bd, b.device_data());
                 Slot &sa = slot(0);
-                rc = katsu_hip_gemm_f32_dev(g, bd, sa.buf.get(), m, k, n, 0, 1, sa.beta(), st);
+                const float beta_a = sa.beta();
                 sa.zero = false;
                 Slot &sb = slot(1);
-                if (rc == KATSU_OK)
-                    rc = katsu_hip_gemm_f32_dev(ad, g, sb.buf.get(), k, n, m, 1, 0, sb.beta(), st);
+                const float beta_b = sb.beta();
                 sb.zero = false;
+                rc = katsu_hip_matmul_vjp_f32_dev(ad, bd, g, sa.buf.get(), sb.buf.get(), m, k, n,
+                                                  beta_a, beta_b, st);
                 break;
             }
         }

@@ -65,8 +65,10 @@ __device__ __forceinline__ float lane_of(const typename FloatN<N>::T &v, int i) 
 // k-tiles g, g + WG, ... through LDS stages of its own, and the groups' sums
 // are added in group order at the end.  Two groups keep two waves on every
 // SIMD when the grid has only about one block per CU.
+// Block `bid` of the `nb` blocks of problem g (gemm_kernel, or one of the
+// two problems of gemm_vjp_kernel).
 template <int BM, int BN, int BK_, bool TA, bool TB, int WG>
-__global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g) {
+__device__ __forceinline__ void gemm_block(const GemmArgs &g, int bid, int nb) {
     using Geo = GemmGeo<BM, BN, BK_, TA, TB>;
     static_assert(WG == 1 || WG == 2, "one or two wave groups");
     constexpr int BK = Geo::BK;
@@ -87,7 +89,7 @@ __global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g
     const int l16 = lane & 15, lg = lane >> 4;
     float *smem = smem_all + grp * 2 * Geo::STAGE;
 
-    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int t = xcd_swizzle(bid, nb);
     const int split = t / (g.tiles_m * g.tiles_n);
     const int tile = t - split * (g.tiles_m * g.tiles_n);
     const int i0 = (tile % g.tiles_m) * BM, j0 = (tile / g.tiles_m) * BN;
@@ -306,6 +308,25 @@ __global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g
                 }
             }
         }
+}
+
+template <int BM, int BN, int BK_, bool TA, bool TB, int WG>
+__global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g) {
+    gemm_block<BM, BN, BK_, TA, TB, WG>(g, blockIdx.x, gridDim.x);
+}
+
+// The matmul VJP's two products in one launch (tensor.rs:424-444): blocks
+// [0, nb0) compute dA = beta*dA + G B^T (NT), the rest dB = beta*dB + A^T G
+// (TN).  The host uses it only when dA and dB do not overlap, so the two
+// results are those of the two launches in the reference's order.  nb0 is a
+// multiple of 8, so each problem's blocks keep their XCD placement.
+template <int BM, int BN, int BK_, int WG>
+__global__ void __launch_bounds__(256 * WG, 2 / WG)
+    gemm_vjp_kernel(const GemmArgs nt, const GemmArgs tn, int nb0) {
+    if ((int)blockIdx.x < nb0)
+        gemm_block<BM, BN, BK_, false, true, WG>(nt, blockIdx.x, nb0);
+    else
+        gemm_block<BM, BN, BK_, true, false, WG>(tn, blockIdx.x - nb0, gridDim.x - nb0);
 }
 
 }  // namespace katsu

@@ -227,10 +227,16 @@ int gemm_fast_wg(const GemmArgs &g, int64_t blocks, int wg, int ta, int tb, hipS
 #define KATSU_GEMM_WG2_BELOW 512
 #endif
 
-// The dedicated GEMM (gemm.hpp) for aligned problems, with a fixed-order
-// reduce of the partial slices when K is split.  False = not applicable.
-bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K, int ta,
-               int tb, float beta, hipStream_t st, int *rc) {
+// The dedicated GEMM (gemm.hpp) for aligned problems: the tile, the split of
+// K and the launch arguments (C not bound yet).  False = not applicable.
+struct GemmFastPlan {
+    GemmArgs g{};
+    int T = 0;
+    int64_t blocks = 0, splits = 1, pstride = 0;
+};
+
+bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, int64_t N,
+                    int64_t K, int ta, int tb, float beta, GemmFastPlan *pl) {
     if (M % 4 || N % 4 || K % 4 || !aligned16(a) || !aligned16(b) || !aligned16(c)) return false;
     if (M * K * 4 >= (int64_t)kMaxBufBytes || K * N * 4 >= (int64_t)kMaxBufBytes ||
         M * N >= kI32Max)
@@ -254,7 +260,7 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     const int64_t kq = T == 128 ? 16 : T == 64 ? KATSU_GEMM_BK64 : 32;  // the tile's k depth
     const int64_t kchunk = (cdiv(K, splits) + kq - 1) / kq * kq;
     splits = cdiv(K, kchunk);
-    GemmArgs g;
+    GemmArgs &g = pl->g;
     g.a = a;
     g.b = b;
     g.M = (int)M;
@@ -270,27 +276,54 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     g.kchunk = (int)kchunk;
     g.a_bytes = (uint32_t)(M * K * 4);
     g.b_bytes = (uint32_t)(K * N * 4);
-    const int64_t pstride = M * N;
+    pl->T = T;
+    pl->splits = splits;
+    pl->pstride = M * N;
+    pl->blocks = tiles * splits;
+    return true;
+}
+
+// The planned GEMM into c, with a fixed-order reduce of the partial slices
+// when K is split.
+bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K, int ta,
+               int tb, float beta, hipStream_t st, int *rc) {
+    GemmFastPlan pl;
+    if (!gemm_fast_plan(a, b, c, M, N, K, ta, tb, beta, &pl)) return false;
+    GemmArgs g = pl.g;
     float *ws = nullptr;
-    if (splits > 1) {
+    if (pl.splits > 1) {
         State &s = state();
         std::lock_guard<std::mutex> lock(s.mu);
-        if ((*rc = ensure(s.gemm_ws, (size_t)(splits * pstride) * sizeof(float))) != KATSU_OK)
+        if ((*rc = ensure(s.gemm_ws, (size_t)(pl.splits * pl.pstride) * sizeof(float))) !=
+            KATSU_OK)
             return true;
         ws = (float *)s.gemm_ws.ptr;
     }
-    g.c = splits > 1 ? ws : c;
-    g.split_stride = splits > 1 ? pstride : 0;
-    const int64_t blocks = tiles * splits;
+    g.c = pl.splits > 1 ? ws : c;
+    g.split_stride = pl.splits > 1 ? pl.pstride : 0;
     // Fewer blocks than two per CU: two wave groups per block, so every SIMD
     // still holds two waves.
-    const int wg = blocks < KATSU_GEMM_WG2_BELOW ? 2 : 1;
-    *rc = T == 128  ? gemm_fast_wg<128, 128, 16>(g, blocks, wg, ta, tb, st)
-          : T == 64 ? gemm_fast_wg<64, 64, KATSU_GEMM_BK64>(g, blocks, wg, ta, tb, st)
-                    : gemm_fast_wg<32, 32, 32>(g, blocks, wg, ta, tb, st);
-    if (*rc == KATSU_OK && splits > 1)
-        *rc = launch_split_reduce(ws, c, M * N, pstride, (int)splits, beta, st);
+    const int wg = pl.blocks < KATSU_GEMM_WG2_BELOW ? 2 : 1;
+    *rc = pl.T == 128  ? gemm_fast_wg<128, 128, 16>(g, pl.blocks, wg, ta, tb, st)
+          : pl.T == 64 ? gemm_fast_wg<64, 64, KATSU_GEMM_BK64>(g, pl.blocks, wg, ta, tb, st)
+                       : gemm_fast_wg<32, 32, 32>(g, pl.blocks, wg, ta, tb, st);
+    if (*rc == KATSU_OK && pl.splits > 1)
+        *rc = launch_split_reduce(ws, c, M * N, pl.pstride, (int)pl.splits, beta, st);
     return true;
+}
+
+// dA and dB of the matmul VJP in one launch (gemm_vjp_kernel).
+template <int BM, int BN, int BK, int WG>
+int gemm_vjp_launch(const GemmArgs &nt, const GemmArgs &tn, int64_t nb0, int64_t nb1,
+                    hipStream_t st) {
+    using GeoNT = GemmGeo<BM, BN, BK, false, true>;
+    using GeoTN = GemmGeo<BM, BN, BK, true, false>;
+    constexpr size_t lds = WG * std::max(GeoNT::kBytes, GeoTN::kBytes);
+    constexpr auto kern = gemm_vjp_kernel<BM, BN, BK, WG>;
+    const int rc = lds_optin<kern>(lds);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3((unsigned)(nb0 + nb1)), dim3(256 * WG), lds, st>>>(nt, tn, (int)nb0);
+    return launch_status();
 }
 
 int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_t k, int ta,
@@ -318,6 +351,49 @@ int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_
         return gemm_dispatch<CfgM>(a, b, c, m, n, k, ta, tb, beta, st);
     if (tiles(64, 64) >= 256) return gemm_dispatch<Cfg64>(a, b, c, m, n, k, ta, tb, beta, st);
     return gemm_dispatch<Cfg32>(a, b, c, m, n, k, ta, tb, beta, st);
+}
+
+// Matmul VJP (tensor.rs:418-445): da = beta_a*da + g b^T, then
+// db = beta_b*db + a^T g; a null da or db skips that product.  When both are
+// wanted, their buffers do not overlap, and both plan the same unsplit tile,
+// the two products run as one launch; otherwise as two launches in that
+// order.
+int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, float *db,
+                   size_t m, size_t k, size_t n, float beta_a, float beta_b, hipStream_t st) {
+    if (!beta_ok(beta_a) || !beta_ok(beta_b)) return KATSU_E_INVALID;
+    if ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max)
+        return KATSU_E_INVALID;
+    const int64_t M = (int64_t)m, N = (int64_t)n, K = (int64_t)k;
+    const bool apart = da && db && (da + M * K <= db || db + K * N <= da);
+    if (apart && M > 0 && N > 0 && K > 0 && a && b && g) {
+        GemmFastPlan pa, pb;
+        if (gemm_fast_plan(g, b, da, M, K, N, 0, 1, beta_a, &pa) &&
+            gemm_fast_plan(a, g, db, K, N, M, 1, 0, beta_b, &pb) && pa.T == pb.T &&
+            pa.splits == 1 && pb.splits == 1 && pa.blocks % 8 == 0 &&
+            pa.blocks + pb.blocks <= kI32Max) {
+            pa.g.c = da;
+            pb.g.c = db;
+            pa.g.split_stride = pb.g.split_stride = 0;
+            // Wave groups by the combined grid (two blocks per CU from the
+            // pair where each alone would take two groups): the k-sum order
+            // can then differ from the separate launches', within the f32
+            // bound and the same on every call.
+            const bool two = pa.blocks + pb.blocks < KATSU_GEMM_WG2_BELOW;
+            const int64_t b0 = pa.blocks, b1 = pb.blocks;
+            if (pa.T == 128)
+                return two ? gemm_vjp_launch<128, 128, 16, 2>(pa.g, pb.g, b0, b1, st)
+                           : gemm_vjp_launch<128, 128, 16, 1>(pa.g, pb.g, b0, b1, st);
+            if (pa.T == 64)
+                return two ? gemm_vjp_launch<64, 64, KATSU_GEMM_BK64, 2>(pa.g, pb.g, b0, b1, st)
+                           : gemm_vjp_launch<64, 64, KATSU_GEMM_BK64, 1>(pa.g, pb.g, b0, b1, st);
+            return two ? gemm_vjp_launch<32, 32, 32, 2>(pa.g, pb.g, b0, b1, st)
+                       : gemm_vjp_launch<32, 32, 32, 1>(pa.g, pb.g, b0, b1, st);
+        }
+    }
+    int rc = KATSU_OK;
+    if (da) rc = gemm_dev(g, b, da, m, k, n, 0, 1, beta_a, st);
+    if (rc == KATSU_OK && db) rc = gemm_dev(a, g, db, k, n, m, 1, 0, beta_b, st);
+    return rc;
 }
 
 // ---------------------------------------------------------------------------
@@ -1754,6 +1830,12 @@ int katsu_hip_conv2d_geometry(katsu_conv_geom *g) { return geometry_fill(g); }
 int katsu_hip_gemm_f32_dev(const float *a, const float *b, float *c, size_t m, size_t n,
                            size_t k, int trans_a, int trans_b, float beta, void *stream) {
     return gemm_dev(a, b, c, m, n, k, trans_a, trans_b, beta, (hipStream_t)stream);
+}
+
+int katsu_hip_matmul_vjp_f32_dev(const float *a, const float *b, const float *g, float *da,
+                                 float *db, size_t m, size_t k, size_t n, float beta_a,
+                                 float beta_b, void *stream) {
+    return matmul_vjp_dev(a, b, g, da, db, m, k, n, beta_a, beta_b, (hipStream_t)stream);
 }
 
 int katsu_hip_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,

@@ -124,14 +124,16 @@ def matmul(a, b):
 def matmul_vjp(a, b, g, da, db):
     """Matmul VJP (tensor.rs:418-445): da += g b^T, then db += a^T g.
 
-    da and db may be the same tensor (A and B the same node); the two
-    launches run in order on one stream, as the reference's loops do."""
+    One call of katsu_hip_matmul_vjp_f32_dev: the two products run as one
+    launch when da and db are separate buffers, and in the reference's order
+    when they are the same tensor (A and B the same node)."""
     m, k = a.shape
     n = b.shape[1]
     if m * n == 0 or k == 0:
         return da, db
-    gemm(g, b, m, k, n, trans_b=True, out=da, beta=1.0)
-    gemm(a, g, k, n, m, trans_a=True, out=db, beta=1.0)
+    _dev_f32(a, b, g, da, db)
+    check(lib().katsu_hip_matmul_vjp_f32_dev(_p(a), _p(b), _p(g), _p(da), _p(db), m, k, n,
+                                             1.0, 1.0, _stream()), "matmul_vjp")
     return da, db
 
 

@@ -153,3 +153,65 @@ def test_config2_4096_sampled_rows(dev):
     ref = a.astype(np.float64).sum(axis=0)
     for p in rows:
         assert_within(db[p], np.full(n, ref[p]), np.full(n, col[p]), n, f"dB row {p}")
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (1024, 1024, 1024), (256, 512, 768),
+                                   (64, 128, 96), (1000, 36, 52)])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_vjp_entry_matches_two_gemms(m, k, n, beta, dev):
+    """katsu_hip_matmul_vjp_f32_dev (dA and dB as one launch when both tile
+    plans agree, else two) agrees with the two GEMM calls within the f32
+    dot-product bound (its k-sums may be grouped differently), and gives the
+    same bits when called again."""
+    import torch
+
+    from katsu_amd import ops
+    from katsu_amd._abi import lib
+    a = _t(synth.uniform(61, (m, k)), dev)
+    b = _t(synth.uniform(62, (k, n)), dev)
+    g = _t(synth.uniform(63, (m, n)), dev)
+    da0 = _t(synth.uniform(64, (m, k)), dev)
+    db0 = _t(synth.uniform(65, (k, n)), dev)
+    da, db = da0.clone(), db0.clone()
+    rc = lib().katsu_hip_matmul_vjp_f32_dev(a.data_ptr(), b.data_ptr(), g.data_ptr(),
+                                            da.data_ptr(), db.data_ptr(), m, k, n, beta, beta,
+                                            ops._stream())
+    assert rc == 0
+    da2, db2 = da0.clone(), db0.clone()
+    assert lib().katsu_hip_matmul_vjp_f32_dev(a.data_ptr(), b.data_ptr(), g.data_ptr(),
+                                              da2.data_ptr(), db2.data_ptr(), m, k, n, beta,
+                                              beta, ops._stream()) == 0
+    ra, rb = da0.clone(), db0.clone()
+    ops.gemm(g, b, m, k, n, trans_b=True, out=ra, beta=beta)
+    ops.gemm(a, g, k, n, m, trans_a=True, out=rb, beta=beta)
+    torch.cuda.synchronize()
+    assert torch.equal(da, da2) and torch.equal(db, db2)
+    ab, bb, gb = (t.abs() for t in (a, b, g))
+    sa = ops.gemm(gb, bb, m, k, n, trans_b=True) + beta * da0.abs()
+    sb = ops.gemm(ab, gb, k, n, m, trans_a=True) + beta * db0.abs()
+    torch.cuda.synchronize()
+    # Two f32 evaluations of the same sum: each within the bound of the exact
+    # value, so within twice the bound of each other.
+    assert_within(da.cpu().numpy(), ra.cpu().numpy().astype(np.float64),
+                  2 * sa.cpu().numpy().astype(np.float64), n + 1, "dA")
+    assert_within(db.cpu().numpy(), rb.cpu().numpy().astype(np.float64),
+                  2 * sb.cpu().numpy().astype(np.float64), m + 1, "dB")
+
+
+def test_vjp_entry_null_output(dev):
+    """A NULL dA or dB skips that product and leaves the other as the GEMM."""
+    import torch
+
+    from katsu_amd import ops
+    from katsu_amd._abi import lib
+    m = k = n = 512
+    a, b, g = (_t(synth.uniform(71 + i, (512, 512)), dev) for i in range(3))
+    for which in (0, 1):
+        out = torch.zeros((512, 512), device=dev)
+        ptrs = (out.data_ptr(), None) if which == 0 else (None, out.data_ptr())
+        assert lib().katsu_hip_matmul_vjp_f32_dev(a.data_ptr(), b.data_ptr(), g.data_ptr(),
+                                                  *ptrs, m, k, n, 0.0, 0.0, ops._stream()) == 0
+        ref = ops.gemm(g, b, m, k, n, trans_b=True) if which == 0 else \
+            ops.gemm(a, g, k, n, m, trans_a=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
