@@ -935,13 +935,14 @@ __global__ void __launch_bounds__(256, 2) direct_dw_kernel(const DirectDwArgs a)
 // passes share one ramp and one tail.  Dynamic LDS is the larger of the two
 // needs.
 template <int XKT, int XF, int XCB, int R, int S, int XROWS, int XPITCH, bool XWVEC, int KT,
-          int CT, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
+          int CT, int ROWS, int PITCH, int GPC, int WKF, bool FULL, int XWMODE = 1, int XEPI = 0,
+          bool XRF = false, int XPD = 0>
 __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
                                                             const DirectDwArgs dw, int nbw) {
     if ((int)blockIdx.x < nbw)
         direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(dw, blockIdx.x, nbw);
     else
-        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC>(
+        direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, XWMODE, XEPI, XWVEC, false, XRF, XPD>(
             dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 

@@ -694,17 +694,31 @@ bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
 
 // The stride-2 data gradient in phase form (direct.hpp, WMODE 3): input G,
 // C output channels over the super-pixel grid, all four phases per block.
-bool dx_phases(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
-               hipStream_t st, int *rc) {
+bool dx_phases_problem(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+                       DirectFwdProblem *P) {
     using Tp = Dxs2Taps<DxPh::R, DxPh::S, DxPh::PD>;
     if (d.st != 2 || d.R != DxPh::R || d.S != DxPh::S || d.pad != DxPh::PD || d.C < 16)
         return false;
-    DirectFwdProblem P{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1, -Tp::DYMIN,
-                       -Tp::DXMIN, (d.H + 1) / 2, (d.W + 1) / 2, beta};
-    P.g_c = d.C;
-    P.fh = d.H;
-    P.fw = d.W;
-    return try_direct<DxPh, 3, 3>(P, st, rc);
+    *P = DirectFwdProblem{gy, w, dx, d.N, d.K, d.OH, d.OW, d.C, d.R, d.S, 1, -Tp::DYMIN,
+                          -Tp::DXMIN, (d.H + 1) / 2, (d.W + 1) / 2, beta};
+    P->g_c = d.C;
+    P->fh = d.H;
+    P->fw = d.W;
+    return true;
+}
+
+bool dx_phases_plan(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+                    DirectFwdPlan *pl) {
+    DirectFwdProblem P;
+    return dx_phases_problem(d, gy, w, dx, beta, &P) && P.CO >= DxPh::KT / 2 &&
+           direct_fwd_plan<DxPh::KT, DxPh::F, DxPh::CB, DxPh::R, DxPh::S, DxPh::ROWS, DxPh::PITCH,
+                           3, DxPh::S2, DxPh::RF, DxPh::PD>(P, pl);
+}
+
+bool dx_phases(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+               hipStream_t st, int *rc) {
+    DirectFwdProblem P;
+    return dx_phases_problem(d, gy, w, dx, beta, &P) && try_direct<DxPh, 3, 3>(P, st, rc);
 }
 
 // The stride-2 data gradient as a stride-1 problem over super-pixels (see
@@ -939,13 +953,13 @@ int direct_dw_launch(DirectDwPlan pl, const float *x, const float *gy, float *dw
 
 // dX and dW in one launch (direct_bwd_kernel): the direct dX plan and a
 // direct dW variant with the same filter size.
-template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL,
-          bool XWVEC>
+template <class XV, int XWMODE, int XEPI, int KT, int CT, int R, int S, int ROWS, int PITCH,
+          int GPC, int WKF, bool FULL, bool XWVEC>
 int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
-    using XGeo = DirectFwdGeo<KATSU_FWD_VARIANT, 1>;
-    constexpr auto kern = direct_bwd_kernel<FwdV::KT, FwdV::F, FwdV::CB, R, S, FwdV::ROWS,
-                                            FwdV::PITCH, XWVEC, KT, CT, ROWS, PITCH, GPC, WKF,
-                                            FULL>;
+    using XGeo = DirectFwdGeo<XV::KT, XV::F, XV::CB, XV::R, XV::S, XV::ROWS, XV::PITCH, XWMODE>;
+    constexpr auto kern = direct_bwd_kernel<XV::KT, XV::F, XV::CB, R, S, XV::ROWS, XV::PITCH,
+                                            XWVEC, KT, CT, ROWS, PITCH, GPC, WKF, FULL, XWMODE,
+                                            XEPI, XV::RF, XV::PD>;
     const int rc = lds_optin<kern>(kLdsMax);
     if (rc != KATSU_OK) return rc;
     const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
@@ -954,24 +968,42 @@ int bwd_fused_kernel_launch(const DirectFwdPlan &xp, const DirectDwPlan &wp, hip
     return launch_status();
 }
 
+template <class XV, int XWMODE, int XEPI, int KT, int CT, int R, int S, int ROWS, int PITCH,
+          int GPC, int WKF>
+int bwd_fused_dx(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
+    if (wp.full)
+        return xp.wvec ? bwd_fused_kernel_launch<XV, XWMODE, XEPI, KT, CT, R, S, ROWS, PITCH, GPC,
+                                                 WKF, true, true>(xp, wp, st)
+                       : bwd_fused_kernel_launch<XV, XWMODE, XEPI, KT, CT, R, S, ROWS, PITCH, GPC,
+                                                 WKF, true, false>(xp, wp, st);
+    return xp.wvec ? bwd_fused_kernel_launch<XV, XWMODE, XEPI, KT, CT, R, S, ROWS, PITCH, GPC, WKF,
+                                             false, true>(xp, wp, st)
+                   : bwd_fused_kernel_launch<XV, XWMODE, XEPI, KT, CT, R, S, ROWS, PITCH, GPC, WKF,
+                                             false, false>(xp, wp, st);
+}
+
+// The dX blocks of a shared launch: the stride-1 form (FwdV, WMODE 1) with a
+// stride-1 dW variant, the stride-2 phase form (DxPh, WMODE 3) with a
+// stride-2 one.
 template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
 int bwd_fused_variant(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
-    if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S) {
-        if (wp.full)
-            return xp.wvec
-                ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true, true>(xp, wp, st)
-                : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true, false>(xp, wp, st);
-        return xp.wvec
-            ? bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false, true>(xp, wp, st)
-            : bwd_fused_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false, false>(xp, wp, st);
-    }
+    if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S)
+        return bwd_fused_dx<FwdV, 1, 0, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
+    else if constexpr (ST == 2 && R == DxPh::R && S == DxPh::S)
+        return bwd_fused_dx<DxPh, 3, 3, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
     return KATSU_E_INVALID;
 }
 
-// Whether a dW variant can share a launch with the direct dX kernel.
-bool dw_variant_fusable(int variant) {
-#define KATSU_DW_FUSABLE(id, st, kt, ct, r, s, rows, pitch, gpc, wkf, tb) \
-    if (variant == id) return st != 2 && r == FwdV::R && s == FwdV::S;
+// Whether a dW variant can share a launch with the direct dX kernel of the
+// layer's stride (see bwd_fused_variant).
+#ifndef KATSU_FUSE_S2
+#define KATSU_FUSE_S2 1
+#endif
+bool dw_variant_fusable(int variant, int64_t stride) {
+#define KATSU_DW_FUSABLE(id, st, kt, ct, r, s, rows, pitch, gpc, wkf, tb)            \
+    if (variant == id)                                                               \
+        return stride == 2 ? KATSU_FUSE_S2 && st == 2 && r == DxPh::R && s == DxPh::S \
+                           : st != 2 && r == FwdV::R && s == FwdV::S;
     KATSU_DW_VARIANTS(KATSU_DW_FUSABLE)
 #undef KATSU_DW_FUSABLE
     return false;
@@ -1633,10 +1665,13 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
     DwPlan wpl;
     // One output buffer for both (an engine's pending buffer when input and
     // weights are one node): the two passes run one after the other.
-    const bool fused = dx != dw && d.npix_out > 0 && x && w && gy &&
-                       dx_as_forward(d, gy, w, dx, beta, &P) &&
-                       P.CO >= FwdV::KT && direct_fwd_plan<KATSU_FWD_VARIANT, 1>(P, &xp) &&
-                       (wpl = dw_plan_any(d)).direct.ok && dw_variant_fusable(wpl.direct.variant);
+    const bool xplan =
+        d.st == 2 ? dx_phases_plan(d, gy, w, dx, beta, &xp)
+                  : dx_as_forward(d, gy, w, dx, beta, &P) && P.CO >= FwdV::KT &&
+                        direct_fwd_plan<KATSU_FWD_VARIANT, 1>(P, &xp);
+    const bool fused = dx != dw && d.npix_out > 0 && x && w && gy && xplan &&
+                       (wpl = dw_plan_any(d)).direct.ok &&
+                       dw_variant_fusable(wpl.direct.variant, d.st);
     if (!fused && dx != dw && d.npix_in > 0 && d.npix_out > 0 && x && w && gy && tiny_ok(d)) {
         // Few channels: dX rows and dW partials in one launch, then the reduce.
         const TinyDwPlan tp = tiny_dw_plan(d);

@@ -3,9 +3,11 @@ separate passes.  Where dX and dW share one launch, dX comes from the same
 kernel and summation order as the separate call and must be identical bit for
 bit; dW splits its pixel reduction into half as many partials there, so it
 must agree with the separate call within the bound of two fp32 sums of the
-same products.  Shapes the fused launch does not take (stride 2, small channel
-counts, other filter sizes) go through the separate passes and must match
-them bit for bit.  beta = 1 accumulates into both outputs."""
+same products.  The shared launch takes 3x3 layers at stride 1 (stride-1 dX
+blocks) and stride 2 (phase-form dX blocks) with enough blocks to fill the
+GPU; other shapes (few blocks, small channel counts, other filter sizes) go
+through the separate passes and must match them bit for bit.  beta = 1
+accumulates into both outputs."""
 import numpy as np
 import pytest
 
@@ -21,7 +23,9 @@ CASES = [
     ((32, 64, 30, 30), (64, 64, 3, 3), 1, 1, True),    # rows not a multiple of 4 (masked dW)
     ((32, 80, 28, 28), (96, 80, 3, 3), 1, 1, True),    # channel counts off the tiles
     ((2, 80, 17, 9), (96, 80, 3, 3), 1, 0, False),     # too few blocks to fuse
-    ((4, 128, 28, 28), (256, 128, 3, 3), 2, 1, False),  # stride 2
+    ((4, 128, 28, 28), (256, 128, 3, 3), 2, 1, False),  # stride 2, too few blocks to fuse
+    ((32, 128, 28, 28), (256, 128, 3, 3), 2, 1, True),  # config 4a: phase-form dX + stride-2 dW
+    ((32, 64, 27, 27), (128, 64, 3, 3), 2, 1, True),    # odd sizes
     ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3, False),      # stem-like
     ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0, False),     # 1x1
 ]
