@@ -1138,6 +1138,51 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
     return launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
 }
 
+// dX and dW of a 1x1 layer in one launch (pw_bwd_kernel), then the reduce:
+// the same plans as the two separate calls, so the same bits.  False = the
+// dW block count is not a multiple of 8 (the shared grid would move the dX
+// blocks' XCD placement): the caller runs the separate calls.
+template <int BMX, int BMW>
+int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
+    ax.tiles_m = (int)cdiv(ax.M, BMX);
+    ax.tiles_n = (int)cdiv(ax.N, PwGeo<BMX>::BN);
+    aw.tiles_m = (int)cdiv(aw.M, BMW);
+    aw.tiles_n = (int)cdiv(aw.N, PwGeo<BMW>::BN);
+    const int64_t bx = (int64_t)ax.tiles_m * ax.tiles_n, bw = (int64_t)aw.tiles_m * aw.tiles_n * aw.splits;
+    if (bx + bw > kI32Max) return KATSU_E_INVALID;
+    const size_t lds = std::max(PwGeo<BMX>::kBytes, PwGeo<BMW>::kBytes);
+    pw_bwd_kernel<BMX, BMW><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
+    return launch_status();
+}
+
+bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *dw,
+            const ConvDims &d, const PwDwPlan &pl, float beta, float *ws, hipStream_t st,
+            int *rc) {
+    PwArgs ax = pw_args(d, d.C, d.npix_out, d.K);
+    ax.g = gy;
+    ax.w = w;
+    ax.out = dx;
+    ax.beta = beta;
+    PwArgs aw = pw_args(d, d.K, d.C, d.npix_out);
+    aw.x = x;
+    aw.g = gy;
+    const bool direct = pl.splits == 1;
+    aw.out = direct ? dw : ws;
+    aw.beta = direct ? beta : 0.f;
+    aw.splits = pl.splits;
+    aw.kchunk = pl.kchunk;
+    aw.split_stride = direct ? 0 : pl.pstride;
+    const int bmx = pw_bm(ax.M, ax.N, 1), bmw = pw_bm(aw.M, aw.N, aw.splits);
+    if (cdiv(aw.M, bmw) * cdiv(aw.N, 64) * aw.splits % 8 != 0) return false;
+    *rc = bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64>(ax, aw, st)
+                                 : pw_bwd_launch<64, 32>(ax, aw, st))
+                    : (bmw == 64 ? pw_bwd_launch<32, 64>(ax, aw, st)
+                                 : pw_bwd_launch<32, 32>(ax, aw, st));
+    if (*rc == KATSU_OK && !direct)
+        *rc = launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
+    return true;
+}
+
 // ---------------------------------------------------------------------------
 // The stem forward (stem_fwd_kernel): three input channels, 7x7, rows of at
 // most 112 output pixels.
@@ -1703,6 +1748,23 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
             return launch_split_reduce(wsp, dw, (int64_t)d.K * d.CRS, tp.pstride, (int)tp.blocks,
                                        beta, st);
         }
+    }
+    if (!fused && dx != dw && d.npix_in > 0 && d.npix_out > 0 && x && w && gy && pw_ok(d)) {
+        // 1x1: dX and the dW partials in one launch, then the reduce.
+        const PwDwPlan pp = pw_dw_plan(d);
+        float *wsp = (float *)ws;
+        if (pp.ok && pp.ws_bytes > 0) {
+            if (!wsp) {
+                if (!fallback) return KATSU_E_INVALID;
+                const int rc = ensure(*fallback, pp.ws_bytes);
+                if (rc != KATSU_OK) return rc;
+                wsp = (float *)fallback->ptr;
+            } else if (ws_bytes < pp.ws_bytes) {
+                return KATSU_E_INVALID;
+            }
+        }
+        int rc = KATSU_OK;
+        if (pp.ok && pw_bwd(x, w, gy, dx, dw, d, pp, beta, wsp, st, &rc)) return rc;
     }
     if (!fused) {
         const int rc = conv_bwd_data_dev(gy, w, dx, g, beta, st);

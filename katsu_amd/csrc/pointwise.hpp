@@ -50,8 +50,10 @@ struct PwGeo {
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
 };
 
+// Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
+// passes of pw_bwd_kernel).
 template <int MODE, int BM>
-__global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
+__device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     using Geo = PwGeo<BM>;
     constexpr int BN = Geo::BN, BK = Geo::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -64,7 +66,7 @@ __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
     const int wi0 = (wave >> 1) * WM, wj0 = (wave & 1) * WN;
     const int l16 = lane & 15, lg = lane >> 4;
 
-    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int t = xcd_swizzle(bid, nb);
     const int split = t / (g.tiles_m * g.tiles_n);
     const int tile = t - split * (g.tiles_m * g.tiles_n);
     const int i0 = (tile % g.tiles_m) * BM, j0 = (tile / g.tiles_m) * BN;
@@ -262,6 +264,24 @@ __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
                 }
         }
     }
+}
+
+template <int MODE, int BM>
+__global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
+    pw_block<MODE, BM>(g, blockIdx.x, gridDim.x);
+}
+
+// dX and the dW partials of a 1x1 layer in one launch (conv2d.rs:265-292):
+// blocks [0, nbw) are dW blocks (the longer ones, dispatched first), the
+// rest dX blocks; nbw is a multiple of 8, so each pass keeps its XCD
+// placement.
+template <int BMX, int BMW>
+__global__ void __launch_bounds__(256, 2) pw_bwd_kernel(const PwArgs dx, const PwArgs dw,
+                                                        int nbw) {
+    if ((int)blockIdx.x < nbw)
+        pw_block<2, BMW>(dw, blockIdx.x, nbw);
+    else
+        pw_block<1, BMX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
 }  // namespace katsu
