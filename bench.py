@@ -186,7 +186,7 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one "
-              "GPU (multi-GPU sharding is a design in DESIGN.md, not measured)",
+              "GPU (sharding over several GPUs is designed, not built or measured)",
               file=sys.stderr)
         return 2
 
