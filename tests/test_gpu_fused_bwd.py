@@ -26,7 +26,8 @@ CASES = [
     ((4, 128, 28, 28), (256, 128, 3, 3), 2, 1, False),  # stride 2, too few blocks to fuse
     ((32, 128, 28, 28), (256, 128, 3, 3), 2, 1, True),  # config 4a: phase-form dX + stride-2 dW
     ((32, 64, 27, 27), (128, 64, 3, 3), 2, 1, True),    # odd sizes
-    ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3, False),      # stem-like
+    ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3, False),      # stem-like, too small for its kernels
+    ((16, 3, 224, 224), (64, 3, 7, 7), 2, 3, False),   # the stem's kernels, as two launches
     ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0, False),     # 1x1
 ]
 
