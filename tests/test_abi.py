@@ -85,6 +85,11 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert L.katsu_hip_gemm_f32(p, p, p, 2, 2, 1, 2, 0, 0.0) == _abi.E_INVALID
     # null output
     assert L.katsu_hip_gemm_f32(p, p, None, 2, 2, 1, 0, 0, 0.0) == _abi.E_INVALID
+    # the VJP entry: either beta outside {0, 1}; sizes past the 32-bit index range
+    assert L.katsu_hip_matmul_vjp_f32_dev(p, p, p, p, p, 2, 2, 2, 0.5, 1.0, None) == _abi.E_INVALID
+    assert L.katsu_hip_matmul_vjp_f32_dev(p, p, p, p, p, 2, 2, 2, 1.0, 2.0, None) == _abi.E_INVALID
+    assert L.katsu_hip_matmul_vjp_f32_dev(p, p, p, p, p, 1 << 32, 2, 2, 1.0, 1.0,
+                                          None) == _abi.E_INVALID
     # oh/ow inconsistent with the geometry
     g = _abi.ConvGeom(1, 1, 3, 3, 1, 2, 2, 1, 0, 5, 5)
     assert L.katsu_hip_conv2d_fwd_f32(p, p, p, ctypes.byref(g)) == _abi.E_INVALID
