@@ -57,28 +57,67 @@ __global__ void __launch_bounds__(256) ew_binary(const float *__restrict__ a,
 // y[i] = beta*y[i] + x[i]: an adjoint added into a pending buffer (Add's VJP,
 // and the publication of pending into an existing gradient,
 // tensor.rs:341-360); beta = 0 copies into a buffer still known to be zero.
+template <bool VEC>
 __global__ void __launch_bounds__(256) ew_accumulate(const float *__restrict__ x, float *y,
                                                      int64_t n, float beta) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        y[i] = beta != 0.f ? y[i] + x[i] : x[i];
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        for (int64_t q = i; q < n4; q += stride) {
+            float4 r = reinterpret_cast<const float4 *>(x)[q];
+            float4 *d = reinterpret_cast<float4 *>(y) + q;
+            if (beta != 0.f) {
+                const float4 o = *d;
+                r = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+            }
+            *d = r;
+        }
+        i += n4 << 2;  // the last n % 4 elements, one per thread of the first block
+        if (i >= n || i >= (n4 << 2) + 4) return;
+    }
+    for (; i < n; i += stride) y[i] = beta != 0.f ? y[i] + x[i] : x[i];
 }
 
 // x[i] = v (fresh zero buffers: a kernel, not a memset, so it can sit in a
 // captured graph).
+template <bool VEC>
 __global__ void __launch_bounds__(256) ew_fill(float *x, int64_t n, float v) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = v;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        for (int64_t q = i; q < n4; q += stride)
+            reinterpret_cast<float4 *>(x)[q] = make_float4(v, v, v, v);
+        i += n4 << 2;
+        if (i >= n || i >= (n4 << 2) + 4) return;
+    }
+    for (; i < n; i += stride) x[i] = v;
 }
 
 // y[i] = beta*y[i] + s[0]: Sum's VJP (tensor.rs:410-417) with the scalar
 // adjoint on the device.
+template <bool VEC>
 __global__ void __launch_bounds__(256) ew_add_scalar(const float *__restrict__ s, float *y,
                                                      int64_t n, float beta) {
     const float v = s[0];
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        y[i] = beta != 0.f ? y[i] + v : v;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        for (int64_t q = i; q < n4; q += stride) {
+            float4 *d = reinterpret_cast<float4 *>(y) + q;
+            float4 r = make_float4(v, v, v, v);
+            if (beta != 0.f) {
+                const float4 o = *d;
+                r = make_float4(o.x + v, o.y + v, o.z + v, o.w + v);
+            }
+            *d = r;
+        }
+        i += n4 << 2;
+        if (i >= n || i >= (n4 << 2) + 4) return;
+    }
+    for (; i < n; i += stride) y[i] = beta != 0.f ? y[i] + v : v;
 }
 
 // Block sum of one value per thread, in a fixed tree (wave shuffles, then
@@ -98,12 +137,28 @@ __device__ __forceinline__ float block_sum_256(float v) {
 
 // Sum, pass 1: block b sums elements [b*chunk, (b+1)*chunk), each thread a
 // strided subsequence in order, then the block tree.
+// VEC (chunk a multiple of 4, x 16-byte aligned): each thread takes
+// float4s and adds their elements in order, then the tail of the last chunk.
+template <bool VEC>
 __global__ void __launch_bounds__(256) sum_partials(const float *__restrict__ x, int64_t n,
                                                     int64_t chunk, float *part) {
     const int64_t lo = (int64_t)blockIdx.x * chunk;
     const int64_t hi = lo + chunk < n ? lo + chunk : n;
     float v = 0.f;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) v += x[i];
+    int64_t i = lo + threadIdx.x;
+    if (VEC) {
+        const int64_t h4 = (hi - lo) >> 2;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + lo);
+        for (int64_t q = threadIdx.x; q < h4; q += 256) {
+            const float4 e = x4[q];
+            v += e.x;
+            v += e.y;
+            v += e.z;
+            v += e.w;
+        }
+        i = lo + (h4 << 2) + threadIdx.x;
+    }
+    for (; i < hi; i += 256) v += x[i];
     const float t = block_sum_256(v);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
@@ -119,7 +174,9 @@ __global__ void __launch_bounds__(256) sum_finish(const float *__restrict__ part
 }
 
 // out[r] = (sum_h y[r][h]) / hw: one wave per row (the stem's global
-// average pool, N*C rows of OH*OW).
+// average pool, N*C rows of OH*OW); VEC (hw a multiple of 4, y 16-byte
+// aligned): float4 loads, their elements added in order.
+template <bool VEC>
 __global__ void __launch_bounds__(256) mean_rows(const float *__restrict__ y, int64_t rows,
                                                  int64_t hw, float *out) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -127,21 +184,49 @@ __global__ void __launch_bounds__(256) mean_rows(const float *__restrict__ y, in
     if (r >= rows) return;
     const float *row = y + r * hw;
     float v = 0.f;
-    for (int64_t i = lane; i < hw; i += 64) v += row[i];
+    if (VEC) {
+        const float4 *row4 = reinterpret_cast<const float4 *>(row);
+        for (int64_t i = lane; i < (hw >> 2); i += 64) {
+            const float4 e = row4[i];
+            v += e.x;
+            v += e.y;
+            v += e.z;
+            v += e.w;
+        }
+    } else {
+        for (int64_t i = lane; i < hw; i += 64) v += row[i];
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
     if (lane == 0) out[r] = v / (float)hw;
 }
 
-// dy[r][h] = beta*dy[r][h] + g[r]*scale: the mean-pool's VJP.
-__global__ void __launch_bounds__(256) broadcast_rows(const float *__restrict__ g, int64_t rows,
-                                                      int64_t hw, float scale, float *dy,
-                                                      float beta) {
-    const int64_t n = rows * hw;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const float v = g[i / hw] * scale;
-        dy[i] = beta != 0.f ? dy[i] + v : v;
+// dy[r][h] = beta*dy[r][h] + g[r]*scale: the mean-pool's VJP.  Block b
+// writes part b % bpr (per_block elements, or float4s when VEC: hw a
+// multiple of 4, dy 16-byte aligned) of row b / bpr.
+template <bool VEC>
+__global__ void __launch_bounds__(256) broadcast_rows(const float *__restrict__ g, int64_t hw,
+                                                      int bpr, int64_t per_block, float scale,
+                                                      float *dy, float beta) {
+    const int b = blockIdx.x;
+    const int64_t r = b / bpr;
+    const float v = g[r] * scale;
+    float *row = dy + r * hw;
+    const int64_t w = VEC ? hw >> 2 : hw;  // elements (or float4s) of the row
+    const int64_t lo = (int64_t)(b - (b / bpr) * bpr) * per_block;
+    const int64_t hi = lo + per_block < w ? lo + per_block : w;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+        if (VEC) {
+            float4 *d = reinterpret_cast<float4 *>(row) + i;
+            float4 o = make_float4(v, v, v, v);
+            if (beta != 0.f) {
+                const float4 p = *d;
+                o = make_float4(p.x + v, p.y + v, p.z + v, p.w + v);
+            }
+            *d = o;
+        } else {
+            row[i] = beta != 0.f ? row[i] + v : v;
+        }
     }
 }
 

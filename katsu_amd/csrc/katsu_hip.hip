@@ -2184,15 +2184,22 @@ int katsu_hip_accumulate_f32_dev(const float *x, float *y, size_t n, float beta,
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     if (n == 0) return KATSU_OK;
     if (!x || !y) return KATSU_E_INVALID;
-    ew_accumulate<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, y, (int64_t)n,
-                                                                          beta);
+    const int64_t N = (int64_t)n;
+    if (aligned16(x) && aligned16(y))
+        ew_accumulate<true><<<ew_blocks(cdiv(N, 4)), 256, 0, (hipStream_t)stream>>>(x, y, N, beta);
+    else
+        ew_accumulate<false><<<ew_blocks(N), 256, 0, (hipStream_t)stream>>>(x, y, N, beta);
     return launch_status();
 }
 
 int katsu_hip_fill_f32_dev(float *x, size_t n, float value, void *stream) {
     if (n == 0) return KATSU_OK;
     if (!x) return KATSU_E_INVALID;
-    ew_fill<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(x, (int64_t)n, value);
+    const int64_t N = (int64_t)n;
+    if (aligned16(x))
+        ew_fill<true><<<ew_blocks(cdiv(N, 4)), 256, 0, (hipStream_t)stream>>>(x, N, value);
+    else
+        ew_fill<false><<<ew_blocks(N), 256, 0, (hipStream_t)stream>>>(x, N, value);
     return launch_status();
 }
 
@@ -2201,8 +2208,12 @@ int katsu_hip_add_scalar_f32_dev(const float *s_, float *y, size_t n, float beta
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     if (n == 0) return KATSU_OK;
     if (!s_ || !y) return KATSU_E_INVALID;
-    ew_add_scalar<<<ew_blocks((int64_t)n), 256, 0, (hipStream_t)stream>>>(s_, y, (int64_t)n,
-                                                                          beta);
+    const int64_t N = (int64_t)n;
+    if (aligned16(y))
+        ew_add_scalar<true><<<ew_blocks(cdiv(N, 4)), 256, 0, (hipStream_t)stream>>>(s_, y, N,
+                                                                                   beta);
+    else
+        ew_add_scalar<false><<<ew_blocks(N), 256, 0, (hipStream_t)stream>>>(s_, y, N, beta);
     return launch_status();
 }
 
@@ -2210,7 +2221,7 @@ int katsu_hip_sum_f32_dev(const float *x, size_t n, float *out, float beta, void
     if (!beta_ok(beta) || !out || (n > 0 && !x)) return KATSU_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (n == 0) {  // the empty fold: out = beta*out + 0
-        if (beta == 0.f) ew_fill<<<1, 256, 0, st>>>(out, 1, 0.f);
+        if (beta == 0.f) ew_fill<false><<<1, 256, 0, st>>>(out, 1, 0.f);
         return launch_status();
     }
     // A fixed number of chunks for a given n (at most 1024), so the tree is
@@ -2226,7 +2237,10 @@ int katsu_hip_sum_f32_dev(const float *x, size_t n, float *out, float beta, void
         if (rc) return rc;
         part = (float *)s.sum_scratch.ptr;
     }
-    sum_partials<<<parts, 256, 0, st>>>(x, N, chunk, part);
+    if (chunk % 4 == 0 && aligned16(x))
+        sum_partials<true><<<parts, 256, 0, st>>>(x, N, chunk, part);
+    else
+        sum_partials<false><<<parts, 256, 0, st>>>(x, N, chunk, part);
     sum_finish<<<1, 256, 0, st>>>(part, parts, out, beta);
     return launch_status();
 }
@@ -2235,8 +2249,13 @@ int katsu_hip_mean_rows_f32_dev(const float *y, size_t rows, size_t cols, float 
                                 void *stream) {
     if (rows == 0) return KATSU_OK;
     if (!y || !out || cols == 0) return KATSU_E_INVALID;
-    mean_rows<<<(unsigned)cdiv((int64_t)rows, 4), 256, 0, (hipStream_t)stream>>>(
-        y, (int64_t)rows, (int64_t)cols, out);
+    if (rows > kI32Max) return KATSU_E_INVALID;
+    if (cols % 4 == 0 && aligned16(y))
+        mean_rows<true><<<(unsigned)cdiv((int64_t)rows, 4), 256, 0, (hipStream_t)stream>>>(
+            y, (int64_t)rows, (int64_t)cols, out);
+    else
+        mean_rows<false><<<(unsigned)cdiv((int64_t)rows, 4), 256, 0, (hipStream_t)stream>>>(
+            y, (int64_t)rows, (int64_t)cols, out);
     return launch_status();
 }
 
@@ -2245,9 +2264,19 @@ int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, f
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     if (rows == 0 || cols == 0) return KATSU_OK;
     if (!g || !dy) return KATSU_E_INVALID;
-    const int64_t n = (int64_t)rows * (int64_t)cols;
-    broadcast_rows<<<ew_blocks(n), 256, 0, (hipStream_t)stream>>>(g, (int64_t)rows,
-                                                                  (int64_t)cols, scale, dy, beta);
+    // Parts of at most 4096 elements (or float4s) per block, rows times parts
+    // blocks in all.
+    const bool vec = cols % 4 == 0 && aligned16(dy);
+    const int64_t w = vec ? (int64_t)cols / 4 : (int64_t)cols;
+    const int64_t bpr = cdiv(w, 4096), per = cdiv(w, bpr);
+    if ((int64_t)rows * bpr > kI32Max) return KATSU_E_INVALID;
+    const unsigned blocks = (unsigned)((int64_t)rows * bpr);
+    if (vec)
+        broadcast_rows<true><<<blocks, 256, 0, (hipStream_t)stream>>>(g, (int64_t)cols, (int)bpr,
+                                                                      per, scale, dy, beta);
+    else
+        broadcast_rows<false><<<blocks, 256, 0, (hipStream_t)stream>>>(g, (int64_t)cols, (int)bpr,
+                                                                       per, scale, dy, beta);
     return launch_status();
 }
 
@@ -2266,7 +2295,10 @@ int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, siz
         if (rc) return rc;
         alpha = (float *)s.cam_scratch.ptr;
     }
-    mean_rows<<<(unsigned)cdiv(N * C, 4), 256, 0, st>>>(grad, N * C, HW, alpha);
+    if (HW % 4 == 0 && aligned16(grad))
+        mean_rows<true><<<(unsigned)cdiv(N * C, 4), 256, 0, st>>>(grad, N * C, HW, alpha);
+    else
+        mean_rows<false><<<(unsigned)cdiv(N * C, 4), 256, 0, st>>>(grad, N * C, HW, alpha);
     cam_combine<<<ew_blocks(N * HW), 256, 0, st>>>(act, alpha, N, C, HW, cam);
     normalize_rows_by_max<<<(unsigned)N, 256, 0, st>>>(cam, HW);
     return launch_status();
