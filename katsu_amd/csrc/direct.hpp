@@ -842,18 +842,48 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                         __builtin_amdgcn_mfma_f32_16x16x4f32(am, b[tap], acc[f][tap], 0, 0, 0);
             }
         };
-        float a0[WKF], a1[WKF], b0[RS], b1[RS];
-        bool k0ok, k1ok;
-        fetch(a0, b0, k0ok);
-        asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
-        for (int s = 0; s < nsteps; s += 2) {
-            fetch(a1, b1, k1ok);
-            mma(a0, b0, k0ok);
-            order_reads_then_mfma<WKF + RS, WKF * RS>();
-            if (s + 1 >= nsteps) break;
-            fetch(a0, b0, k0ok);
-            mma(a1, b1, k1ok);
-            order_reads_then_mfma<WKF + RS, WKF * RS>();
+        auto run = [&](auto &&fetchf, const int nst) __attribute__((always_inline)) {
+            float a0[WKF], a1[WKF], b0[RS], b1[RS];
+            bool k0ok, k1ok;
+            fetchf(a0, b0, k0ok);
+            asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
+            for (int s = 0; s < nst; s += 2) {
+                fetchf(a1, b1, k1ok);
+                mma(a0, b0, k0ok);
+                order_reads_then_mfma<WKF + RS, WKF * RS>();
+                if (s + 1 >= nst) break;
+                fetchf(a0, b0, k0ok);
+                mma(a1, b1, k1ok);
+                order_reads_then_mfma<WKF + RS, WKF * RS>();
+            }
+        };
+        if (!FULL && a.segs == 1 && a.OW >= 4) {
+            // Tiles of whole rows whose width is not a multiple of 4: steps
+            // over the tile's flattened pixels (G is stored contiguous by
+            // pixel), so only the tile's last step has idle lanes.  Each lane
+            // keeps its pixel's (row, column) for the X reads.
+            int q = lq, prow = lq / a.OW, pcol = lq - (lq / a.OW) * a.OW;
+            auto ffetch = [&](float (&av)[WKF], float (&b)[RS], bool &ok)
+                __attribute__((always_inline)) {
+                ok = q < tg.np;
+                const int row = min(prow, tg.tr - 1), col = ok ? pcol : a.OW - 1;
+                const float *gsrc = base + arow + min(q, tg.np - 1);
+#pragma unroll
+                for (int f = 0; f < WKF; ++f) av[f] = gsrc[f * 16 * a.gpitch];
+                const float *xs = base + bch + row * a.st * Geo::PITCH + col * a.st;
+#pragma unroll
+                for (int tap = 0; tap < RS; ++tap)
+                    b[tap] = xs[(tap / S) * Geo::PITCH + tap % S];
+                q += 4;
+                pcol += 4;
+                if (pcol >= a.OW) {
+                    pcol -= a.OW;
+                    ++prow;
+                }
+            };
+            run(ffetch, (tg.np + 3) >> 2);
+        } else {
+            run(fetch, nsteps);
         }
     };
     if (tb < te) {
