@@ -5,8 +5,9 @@ bit; dW splits its pixel reduction into half as many partials there, so it
 must agree with the separate call within the bound of two fp32 sums of the
 same products.  The shared launch takes 3x3 layers at stride 1 (stride-1 dX
 blocks) and stride 2 (phase-form dX blocks) with enough blocks to fill the
-GPU; other shapes (few blocks, small channel counts, other filter sizes) go
-through the separate passes and must match them bit for bit.  beta = 1
+GPU.  Unpadded 1x1 layers share one launch with the separate passes' own
+plans; they and the other shapes (few blocks, small channel counts, other
+filter sizes) must match the separate passes bit for bit.  beta = 1
 accumulates into both outputs."""
 import numpy as np
 import pytest
@@ -29,6 +30,8 @@ CASES = [
     ((2, 3, 40, 40), (64, 3, 7, 7), 2, 3, False),      # stem-like, too small for its kernels
     ((16, 3, 224, 224), (64, 3, 7, 7), 2, 3, False),   # the stem's kernels, as two launches
     ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0, False),     # 1x1
+    ((32, 128, 28, 28), (256, 128, 1, 1), 2, 0, False),  # config 4b: one pw_bwd_kernel launch
+    ((6, 40, 15, 17), (24, 40, 1, 1), 2, 0, False),    # 1x1 stride 2, odd sizes
 ]
 
 
