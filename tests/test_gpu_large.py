@@ -37,7 +37,10 @@ def test_convolution_image_over_1gib(dev):
     y = ops.conv2d_forward(xd, wd, st, p).cpu().numpy()
     dx = ops.conv2d_backward_data(gd, wd, xs, st, p).cpu().numpy()
     dw = ops.conv2d_backward_filter(xd, gd, ws, st, p).cpu().numpy()
-    del xd, gd
+    # The one-call backward runs the same plans: the same bits.
+    bdx, bdw = ops.conv2d_backward(xd, wd, gd, st, p)
+    assert np.array_equal(bdx.cpu().numpy(), dx) and np.array_equal(bdw.cpu().numpy(), dw)
+    del xd, gd, bdx, bdw
     k, c, r, s = ws
     pts = random_samples(gs, 200, 1) + edge_samples(gs)
     ref, sab = sample_fwd(x, w, st, p, pts)
