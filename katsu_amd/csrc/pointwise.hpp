@@ -52,7 +52,7 @@ struct PwGeo {
 
 // Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
 // passes of pw_bwd_kernel).
-template <int MODE, int BM>
+template <int MODE, int BM, bool AV>
 __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     using Geo = PwGeo<BM>;
     constexpr int BN = Geo::BN, BK = Geo::BK;
@@ -60,6 +60,7 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     constexpr int FM = WM / 16, FN = WN / 16;
     constexpr int NA = BM * BK / 256, NB = BN * BK / 256;  // elements per thread per k-tile
     static_assert(BM == 32 || BM == 64, "BM");
+    static_assert(!AV || MODE != 2, "16-byte weight loads: forward and dX only");
 
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -95,29 +96,44 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
 
     float va[NA], vb[NB];
     auto load = [&](int k0) __attribute__((always_inline)) {
-        if (MODE == 0) {
+        if (MODE != 2) {
+            // A: the weight, w[o][c] with c contiguous; 16 bytes at a time
+            // (four k of one row in MODE 0, four rows i of one k in MODE 1)
+            // when the host found C % 4 == 0 and w 16-byte aligned.
+            if (AV) {
 #pragma unroll
-            for (int q = 0; q < NA; ++q) {  // w[o][c], c fastest
-                const int e = q * 256 + tid;
-                const int i = i0 + e / BK, k = k0 + e % BK;
-                va[q] = (i < g.M && k < ke) ? g.w[(int64_t)i * g.C + k] : 0.f;
+                for (int q = 0; q < NA / 4; ++q) {
+                    const int e = q * 256 + tid;
+                    int i, k;
+                    if (MODE == 0) { i = i0 + e / (BK / 4); k = k0 + 4 * (e % (BK / 4)); }
+                    else { i = i0 + 4 * (e % (BM / 4)); k = k0 + e / (BM / 4); }
+                    const int64_t off = MODE == 0 ? (int64_t)i * g.C + k : (int64_t)k * g.C + i;
+                    const floatx4 v = (i < g.M && k < ke)
+                                          ? *reinterpret_cast<const floatx4 *>(g.w + off)
+                                          : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) va[4 * q + r] = v[r];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < NA; ++q) {
+                    const int e = q * 256 + tid;
+                    if (MODE == 0) {
+                        const int i = i0 + e / BK, k = k0 + e % BK;
+                        va[q] = (i < g.M && k < ke) ? g.w[(int64_t)i * g.C + k] : 0.f;
+                    } else {
+                        const int i = i0 + e % BM, k = k0 + e / BM;
+                        va[q] = (i < g.M && k < ke) ? g.w[(int64_t)k * g.C + i] : 0.f;
+                    }
+                }
             }
+            // B: pixel columns, x[n][c][oy*s][ox*s] (MODE 0) or G[n][o][p].
 #pragma unroll
-            for (int q = 0; q < NB; ++q) {  // x[n][c][oy*s][ox*s]
+            for (int q = 0; q < NB; ++q) {
                 const int k = k0 + q * 4 + (tid >> 6);
-                vb[q] = (colok && k < ke) ? g.x[colx + (int64_t)k * g.HW] : 0.f;
-            }
-        } else if (MODE == 1) {
-#pragma unroll
-            for (int q = 0; q < NA; ++q) {  // w[o][c], c fastest
-                const int e = q * 256 + tid;
-                const int i = i0 + e % BM, k = k0 + e / BM;
-                va[q] = (i < g.M && k < ke) ? g.w[(int64_t)k * g.C + i] : 0.f;
-            }
-#pragma unroll
-            for (int q = 0; q < NB; ++q) {  // G[n][o][p]
-                const int k = k0 + q * 4 + (tid >> 6);
-                vb[q] = (colok && k < ke) ? g.g[colg + (int64_t)k * g.OHW] : 0.f;
+                vb[q] = (colok && k < ke)
+                            ? (MODE == 0 ? g.x[colx + (int64_t)k * g.HW] : g.g[colg + (int64_t)k * g.OHW])
+                            : 0.f;
             }
         } else {
             // One pixel per thread per k-tile: k = k0 + tid % 32.
@@ -146,11 +162,17 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
         float *sa = st, *sb = st + Geo::SA;
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
-            const int e = q * 256 + tid;
             int i, k;
-            if (MODE == 0) { i = e / BK; k = e % BK; }
-            else if (MODE == 1) { i = e % BM; k = e / BM; }
-            else { i = q * (256 / BK) + tid / BK; k = tid & (BK - 1); }
+            if (AV) {
+                const int e = (q / 4) * 256 + tid, r = q % 4;
+                if (MODE == 0) { i = e / (BK / 4); k = 4 * (e % (BK / 4)) + r; }
+                else { i = 4 * (e % (BM / 4)) + r; k = e / (BM / 4); }
+            } else {
+                const int e = q * 256 + tid;
+                if (MODE == 0) { i = e / BK; k = e % BK; }
+                else if (MODE == 1) { i = e % BM; k = e / BM; }
+                else { i = q * (256 / BK) + tid / BK; k = tid & (BK - 1); }
+            }
             sa[k * Geo::PA + i] = va[q];
         }
 #pragma unroll
@@ -266,22 +288,22 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     }
 }
 
-template <int MODE, int BM>
+template <int MODE, int BM, bool AV>
 __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
-    pw_block<MODE, BM>(g, blockIdx.x, gridDim.x);
+    pw_block<MODE, BM, AV>(g, blockIdx.x, gridDim.x);
 }
 
 // dX and the dW partials of a 1x1 layer in one launch (conv2d.rs:265-292):
 // blocks [0, nbw) are dW blocks (the longer ones, dispatched first), the
 // rest dX blocks; nbw is a multiple of 8, so each pass keeps its XCD
 // placement.
-template <int BMX, int BMW>
+template <int BMX, int BMW, bool AVX>
 __global__ void __launch_bounds__(256, 2) pw_bwd_kernel(const PwArgs dx, const PwArgs dw,
                                                         int nbw) {
     if ((int)blockIdx.x < nbw)
-        pw_block<2, BMW>(dw, blockIdx.x, nbw);
+        pw_block<2, BMW, false>(dw, blockIdx.x, nbw);
     else
-        pw_block<1, BMX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
+        pw_block<1, BMX, AVX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
 }  // namespace katsu
