@@ -1060,31 +1060,37 @@ int pw_bm(int64_t m, int64_t n, int64_t splits) {
     return cdiv(m, 64) * cdiv(n, 64) * splits >= kMinDirectBlocks ? 64 : 32;
 }
 
-template <int MODE, int BM, bool AV>
+template <int MODE, int BM, int V>
 int pw_launch(PwArgs a, hipStream_t st) {
     a.tiles_m = (int)cdiv(a.M, BM);
     a.tiles_n = (int)cdiv(a.N, PwGeo<BM>::BN);
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * a.splits;
     if (blocks <= 0) return KATSU_OK;
     if (blocks > kI32Max) return KATSU_E_INVALID;
-    pw_kernel<MODE, BM, AV><<<dim3((unsigned)blocks), dim3(256), PwGeo<BM>::kBytes, st>>>(a);
+    pw_kernel<MODE, BM, V><<<dim3((unsigned)blocks), dim3(256), PwGeo<BM>::kBytes, st>>>(a);
     return launch_status();
 }
 
-// 16-byte weight loads (forward and dX): rows of w whose length C is a
-// multiple of 4, from a 16-byte aligned base.
-bool pw_av(const PwArgs &a) { return a.C % 4 == 0 && aligned16(a.w); }
+// Vector loads of pw_kernel (forward and dX): 1 = the weight 16 bytes at a
+// time (rows of length C % 4 = 0 from a 16-byte aligned base); 3 = also G
+// in the dX (planes of OH*OW % 4 = 0 floats from a 16-byte aligned base).
+int pw_vec(const PwArgs &a, int mode) {
+    if (mode == 2 || a.C % 4 != 0 || !aligned16(a.w)) return 0;
+    return mode == 1 && a.OHW % 4 == 0 && aligned16(a.g) ? 3 : 1;
+}
 
-template <int MODE, bool AV>
-int pw_run_av(const PwArgs &a, hipStream_t st) {
-    return pw_bm(a.M, a.N, a.splits) == 64 ? pw_launch<MODE, 64, AV>(a, st)
-                                             : pw_launch<MODE, 32, AV>(a, st);
+template <int MODE, int V>
+int pw_run_v(const PwArgs &a, hipStream_t st) {
+    return pw_bm(a.M, a.N, a.splits) == 64 ? pw_launch<MODE, 64, V>(a, st)
+                                             : pw_launch<MODE, 32, V>(a, st);
 }
 
 template <int MODE>
 int pw_run(const PwArgs &a, hipStream_t st) {
-    if (MODE != 2 && pw_av(a)) return pw_run_av<MODE, MODE != 2>(a, st);
-    return pw_run_av<MODE, false>(a, st);
+    const int v = pw_vec(a, MODE);
+    if (MODE == 1 && v == 3) return pw_run_v<MODE, MODE == 1 ? 3 : 0>(a, st);
+    if (MODE != 2 && v == 1) return pw_run_v<MODE, MODE != 2 ? 1 : 0>(a, st);
+    return pw_run_v<MODE, 0>(a, st);
 }
 
 int pw_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
@@ -1152,7 +1158,7 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
 // the same plans as the two separate calls, so the same bits.  False = the
 // dW block count is not a multiple of 8 (the shared grid would move the dX
 // blocks' XCD placement): the caller runs the separate calls.
-template <int BMX, int BMW, bool AVX>
+template <int BMX, int BMW, int VX>
 int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     ax.tiles_m = (int)cdiv(ax.M, BMX);
     ax.tiles_n = (int)cdiv(ax.N, PwGeo<BMX>::BN);
@@ -1161,16 +1167,16 @@ int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     const int64_t bx = (int64_t)ax.tiles_m * ax.tiles_n, bw = (int64_t)aw.tiles_m * aw.tiles_n * aw.splits;
     if (bx + bw > kI32Max) return KATSU_E_INVALID;
     const size_t lds = std::max(PwGeo<BMX>::kBytes, PwGeo<BMW>::kBytes);
-    pw_bwd_kernel<BMX, BMW, AVX><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
+    pw_bwd_kernel<BMX, BMW, VX><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
     return launch_status();
 }
 
-template <bool AVX>
+template <int VX>
 int pw_bwd_bm(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
-    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, AVX>(ax, aw, st)
-                                  : pw_bwd_launch<64, 32, AVX>(ax, aw, st))
-                     : (bmw == 64 ? pw_bwd_launch<32, 64, AVX>(ax, aw, st)
-                                  : pw_bwd_launch<32, 32, AVX>(ax, aw, st));
+    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, VX>(ax, aw, st)
+                                  : pw_bwd_launch<64, 32, VX>(ax, aw, st))
+                     : (bmw == 64 ? pw_bwd_launch<32, 64, VX>(ax, aw, st)
+                                  : pw_bwd_launch<32, 32, VX>(ax, aw, st));
 }
 
 bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *dw,
@@ -1192,7 +1198,10 @@ bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *d
     aw.split_stride = direct ? 0 : pl.pstride;
     const int bmx = pw_bm(ax.M, ax.N, 1), bmw = pw_bm(aw.M, aw.N, aw.splits);
     if (cdiv(aw.M, bmw) * cdiv(aw.N, 64) * aw.splits % 8 != 0) return false;
-    *rc = pw_av(ax) ? pw_bwd_bm<true>(bmx, bmw, ax, aw, st) : pw_bwd_bm<false>(bmx, bmw, ax, aw, st);
+    const int vx = pw_vec(ax, 1);
+    *rc = vx == 3   ? pw_bwd_bm<3>(bmx, bmw, ax, aw, st)
+          : vx == 1 ? pw_bwd_bm<1>(bmx, bmw, ax, aw, st)
+                    : pw_bwd_bm<0>(bmx, bmw, ax, aw, st);
     if (*rc == KATSU_OK && !direct)
         *rc = launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
     return true;

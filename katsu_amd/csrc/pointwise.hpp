@@ -52,8 +52,12 @@ struct PwGeo {
 
 // Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
 // passes of pw_bwd_kernel).
-template <int MODE, int BM, bool AV>
+// V: 0 scalar loads; 1 the weight 16 bytes at a time (C % 4 = 0, w 16-byte
+// aligned); 3 also G 16 bytes at a time in MODE 1 (OH*OW % 4 = 0, G 16-byte
+// aligned), each thread then taking four adjacent pixel columns.
+template <int MODE, int BM, int V>
 __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
+    constexpr bool AV = (V & 1) != 0, BV = MODE == 1 && (V & 2) != 0;
     using Geo = PwGeo<BM>;
     constexpr int BN = Geo::BN, BK = Geo::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -79,11 +83,12 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     //   MODE 0: A (o, c) c-fast; B (c, pixel) pixel-fast
     //   MODE 1: A (c, o) c-fast (i-fast); B (o, pixel) pixel-fast
     //   MODE 2: A (o, pixel) pixel-fast (k-fast); B (pixel, c) pixel-fast (k-fast)
-    // Pixel columns of MODE 0 and 1: this thread's column is j0 + tid % 64.
+    // Pixel columns of MODE 0 and 1: this thread's column is j0 + tid % 64
+    // (with BV, columns j0 + 4*(tid % 16) .. +3, all in one image).
     int64_t colx = 0, colg = 0;
     bool colok = false;
     if (MODE != 2) {
-        const int j = j0 + (tid & 63);
+        const int j = j0 + (BV ? 4 * (tid & 15) : (tid & 63));
         colok = j < g.N;
         const int jj = colok ? j : 0;
         const int n = g.fd_ohw.div(jj);
@@ -128,12 +133,25 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
                 }
             }
             // B: pixel columns, x[n][c][oy*s][ox*s] (MODE 0) or G[n][o][p].
+            if (BV) {
 #pragma unroll
-            for (int q = 0; q < NB; ++q) {
-                const int k = k0 + q * 4 + (tid >> 6);
-                vb[q] = (colok && k < ke)
-                            ? (MODE == 0 ? g.x[colx + (int64_t)k * g.HW] : g.g[colg + (int64_t)k * g.OHW])
-                            : 0.f;
+                for (int q = 0; q < NB / 4; ++q) {
+                    const int k = k0 + q * 16 + (tid >> 4);
+                    const floatx4 v =
+                        (colok && k < ke)
+                            ? *reinterpret_cast<const floatx4 *>(g.g + colg + (int64_t)k * g.OHW)
+                            : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) vb[4 * q + r] = v[r];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < NB; ++q) {
+                    const int k = k0 + q * 4 + (tid >> 6);
+                    vb[q] = (colok && k < ke) ? (MODE == 0 ? g.x[colx + (int64_t)k * g.HW]
+                                                           : g.g[colg + (int64_t)k * g.OHW])
+                                              : 0.f;
+                }
             }
         } else {
             // One pixel per thread per k-tile: k = k0 + tid % 32.
@@ -178,7 +196,8 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
             int j, k;
-            if (MODE != 2) { j = tid & 63; k = q * 4 + (tid >> 6); }
+            if (BV) { j = 4 * (tid & 15) + q % 4; k = (q / 4) * 16 + (tid >> 4); }
+            else if (MODE != 2) { j = tid & 63; k = q * 4 + (tid >> 6); }
             else { j = q * (256 / BK) + tid / BK; k = tid & (BK - 1); }
             sb[k * Geo::PB + j] = vb[q];
         }
@@ -288,22 +307,22 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     }
 }
 
-template <int MODE, int BM, bool AV>
+template <int MODE, int BM, int V>
 __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
-    pw_block<MODE, BM, AV>(g, blockIdx.x, gridDim.x);
+    pw_block<MODE, BM, V>(g, blockIdx.x, gridDim.x);
 }
 
 // dX and the dW partials of a 1x1 layer in one launch (conv2d.rs:265-292):
 // blocks [0, nbw) are dW blocks (the longer ones, dispatched first), the
 // rest dX blocks; nbw is a multiple of 8, so each pass keeps its XCD
 // placement.
-template <int BMX, int BMW, bool AVX>
+template <int BMX, int BMW, int VX>
 __global__ void __launch_bounds__(256, 2) pw_bwd_kernel(const PwArgs dx, const PwArgs dw,
                                                         int nbw) {
     if ((int)blockIdx.x < nbw)
-        pw_block<2, BMW, false>(dw, blockIdx.x, nbw);
+        pw_block<2, BMW, 0>(dw, blockIdx.x, nbw);
     else
-        pw_block<1, BMX, AVX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
+        pw_block<1, BMX, VX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
 }  // namespace katsu
