@@ -1071,12 +1071,15 @@ int pw_launch(PwArgs a, hipStream_t st) {
     return launch_status();
 }
 
-// Vector loads of pw_kernel (forward and dX): 1 = the weight 16 bytes at a
-// time (rows of length C % 4 = 0 from a 16-byte aligned base); 3 = also G
-// in the dX (planes of OH*OW % 4 = 0 floats from a 16-byte aligned base).
+// Vector loads of pw_kernel: 1 = the A operand 16 bytes at a time (forward
+// and dX: the weight, rows of length C % 4 = 0 from a 16-byte aligned base;
+// dW: G along pixels, planes of OH*OW % 4 = 0 floats from a 16-byte aligned
+// base); 3 = the dX's G too (the same plane condition).
 int pw_vec(const PwArgs &a, int mode) {
-    if (mode == 2 || a.C % 4 != 0 || !aligned16(a.w)) return 0;
-    return mode == 1 && a.OHW % 4 == 0 && aligned16(a.g) ? 3 : 1;
+    const bool gv = a.OHW % 4 == 0 && aligned16(a.g);
+    if (mode == 2) return gv ? 1 : 0;
+    if (a.C % 4 != 0 || !aligned16(a.w)) return 0;
+    return mode == 1 && gv ? 3 : 1;
 }
 
 template <int MODE, int V>
@@ -1089,7 +1092,7 @@ template <int MODE>
 int pw_run(const PwArgs &a, hipStream_t st) {
     const int v = pw_vec(a, MODE);
     if (MODE == 1 && v == 3) return pw_run_v<MODE, MODE == 1 ? 3 : 0>(a, st);
-    if (MODE != 2 && v == 1) return pw_run_v<MODE, MODE != 2 ? 1 : 0>(a, st);
+    if (v == 1) return pw_run_v<MODE, 1>(a, st);
     return pw_run_v<MODE, 0>(a, st);
 }
 
@@ -1158,7 +1161,7 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
 // the same plans as the two separate calls, so the same bits.  False = the
 // dW block count is not a multiple of 8 (the shared grid would move the dX
 // blocks' XCD placement): the caller runs the separate calls.
-template <int BMX, int BMW, int VX>
+template <int BMX, int BMW, int VX, int VW>
 int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     ax.tiles_m = (int)cdiv(ax.M, BMX);
     ax.tiles_n = (int)cdiv(ax.N, PwGeo<BMX>::BN);
@@ -1167,16 +1170,22 @@ int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     const int64_t bx = (int64_t)ax.tiles_m * ax.tiles_n, bw = (int64_t)aw.tiles_m * aw.tiles_n * aw.splits;
     if (bx + bw > kI32Max) return KATSU_E_INVALID;
     const size_t lds = std::max(PwGeo<BMX>::kBytes, PwGeo<BMW>::kBytes);
-    pw_bwd_kernel<BMX, BMW, VX><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
+    pw_bwd_kernel<BMX, BMW, VX, VW><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
     return launch_status();
 }
 
-template <int VX>
+template <int VX, int VW>
 int pw_bwd_bm(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
-    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, VX>(ax, aw, st)
-                                  : pw_bwd_launch<64, 32, VX>(ax, aw, st))
-                     : (bmw == 64 ? pw_bwd_launch<32, 64, VX>(ax, aw, st)
-                                  : pw_bwd_launch<32, 32, VX>(ax, aw, st));
+    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, VX, VW>(ax, aw, st)
+                                  : pw_bwd_launch<64, 32, VX, VW>(ax, aw, st))
+                     : (bmw == 64 ? pw_bwd_launch<32, 64, VX, VW>(ax, aw, st)
+                                  : pw_bwd_launch<32, 32, VX, VW>(ax, aw, st));
+}
+
+template <int VX>
+int pw_bwd_vw(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
+    return pw_vec(aw, 2) == 1 ? pw_bwd_bm<VX, 1>(bmx, bmw, ax, aw, st)
+                              : pw_bwd_bm<VX, 0>(bmx, bmw, ax, aw, st);
 }
 
 bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *dw,
@@ -1199,9 +1208,9 @@ bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *d
     const int bmx = pw_bm(ax.M, ax.N, 1), bmw = pw_bm(aw.M, aw.N, aw.splits);
     if (cdiv(aw.M, bmw) * cdiv(aw.N, 64) * aw.splits % 8 != 0) return false;
     const int vx = pw_vec(ax, 1);
-    *rc = vx == 3   ? pw_bwd_bm<3>(bmx, bmw, ax, aw, st)
-          : vx == 1 ? pw_bwd_bm<1>(bmx, bmw, ax, aw, st)
-                    : pw_bwd_bm<0>(bmx, bmw, ax, aw, st);
+    *rc = vx == 3   ? pw_bwd_vw<3>(bmx, bmw, ax, aw, st)
+          : vx == 1 ? pw_bwd_vw<1>(bmx, bmw, ax, aw, st)
+                    : pw_bwd_vw<0>(bmx, bmw, ax, aw, st);
     if (*rc == KATSU_OK && !direct)
         *rc = launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
     return true;

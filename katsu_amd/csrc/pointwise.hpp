@@ -52,9 +52,11 @@ struct PwGeo {
 
 // Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
 // passes of pw_bwd_kernel).
-// V: 0 scalar loads; 1 the weight 16 bytes at a time (C % 4 = 0, w 16-byte
-// aligned); 3 also G 16 bytes at a time in MODE 1 (OH*OW % 4 = 0, G 16-byte
-// aligned), each thread then taking four adjacent pixel columns.
+// V: 0 scalar loads; bit 0 the A operand 16 bytes at a time (the weight in
+// MODE 0 and 1: C % 4 = 0, w 16-byte aligned; G along four adjacent pixels
+// in MODE 2: OH*OW % 4 = 0, G 16-byte aligned); V = 3 also G 16 bytes at a
+// time in MODE 1 (same condition), each thread then taking four adjacent
+// pixel columns.
 template <int MODE, int BM, int V>
 __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     constexpr bool AV = (V & 1) != 0, BV = MODE == 1 && (V & 2) != 0;
@@ -64,7 +66,6 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     constexpr int FM = WM / 16, FN = WN / 16;
     constexpr int NA = BM * BK / 256, NB = BN * BK / 256;  // elements per thread per k-tile
     static_assert(BM == 32 || BM == 64, "BM");
-    static_assert(!AV || MODE != 2, "16-byte weight loads: forward and dX only");
 
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -164,10 +165,28 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
             const int ox = p - oy * g.OW;
             const int64_t gb = (int64_t)n * g.g_img + p;
             const int64_t xb = (int64_t)n * g.x_img + (int64_t)oy * g.st * g.W + (int64_t)ox * g.st;
+            if (AV) {  // G[n][o][p..p+3]: pixels k4 .. k4+3 of one image
+                const int k4 = k0 + 4 * (tid & (BK / 4 - 1));
+                const bool k4ok = k4 < ke;
+                const int kk4 = k4ok ? k4 : 0;
+                const int n4 = g.fd_ohw.div(kk4);
+                const int64_t gb4 = (int64_t)n4 * g.g_img + (kk4 - n4 * g.OHW);
 #pragma unroll
-            for (int q = 0; q < NA; ++q) {  // G[n][o][p]
-                const int i = i0 + q * (256 / BK) + (tid / BK);
-                va[q] = (kok && i < g.M) ? g.g[gb + (int64_t)i * g.OHW] : 0.f;
+                for (int q = 0; q < NA / 4; ++q) {
+                    const int i = i0 + q * (1024 / BK) + (tid / (BK / 4));
+                    const floatx4 v =
+                        (k4ok && i < g.M)
+                            ? *reinterpret_cast<const floatx4 *>(g.g + gb4 + (int64_t)i * g.OHW)
+                            : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) va[4 * q + r] = v[r];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < NA; ++q) {  // G[n][o][p]
+                    const int i = i0 + q * (256 / BK) + (tid / BK);
+                    va[q] = (kok && i < g.M) ? g.g[gb + (int64_t)i * g.OHW] : 0.f;
+                }
             }
 #pragma unroll
             for (int q = 0; q < NB; ++q) {  // x[n][c][oy*s][ox*s]
@@ -181,7 +200,10 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
             int i, k;
-            if (AV) {
+            if (AV && MODE == 2) {
+                i = (q / 4) * (1024 / BK) + tid / (BK / 4);
+                k = 4 * (tid & (BK / 4 - 1)) + q % 4;
+            } else if (AV) {
                 const int e = (q / 4) * 256 + tid, r = q % 4;
                 if (MODE == 0) { i = e / (BK / 4); k = 4 * (e % (BK / 4)) + r; }
                 else { i = 4 * (e % (BM / 4)) + r; k = e / (BM / 4); }
@@ -316,11 +338,11 @@ __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
 // blocks [0, nbw) are dW blocks (the longer ones, dispatched first), the
 // rest dX blocks; nbw is a multiple of 8, so each pass keeps its XCD
 // placement.
-template <int BMX, int BMW, int VX>
+template <int BMX, int BMW, int VX, int VW>
 __global__ void __launch_bounds__(256, 2) pw_bwd_kernel(const PwArgs dx, const PwArgs dw,
                                                         int nbw) {
     if ((int)blockIdx.x < nbw)
-        pw_block<2, BMW, 0>(dw, blockIdx.x, nbw);
+        pw_block<2, BMW, VW>(dw, blockIdx.x, nbw);
     else
         pw_block<1, BMX, VX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
