@@ -59,13 +59,15 @@ def capture(fn):
     return g
 
 
-def timed_steps(step, k):
+def timed_steps(step, k, reset=None):
     """Captures `step` STEPS_PER_GRAPH times over in one HIP graph (and the
     remainder of k in a second) and returns the milliseconds that replaying
     exactly k steps takes, and the per-step milliseconds of each full replay
     (events between replays).  Several steps per graph keep the per-replay
     launch cost of a HIP graph out of the per-step time, as a training loop
-    captured whole would."""
+    captured whole would.  `reset` runs after the untimed first replay and
+    before the timed ones (the caller poisons the outputs there, so a check
+    afterwards shows that the timed replays wrote them)."""
     import torch
     per = max(1, min(STEPS_PER_GRAPH, k))
     full, rem = divmod(k, per)
@@ -73,6 +75,9 @@ def timed_steps(step, k):
     g_rem = capture(lambda: [step() for _ in range(rem)]) if rem else None
     g_full.replay()
     torch.cuda.synchronize()
+    if reset is not None:
+        reset()
+        torch.cuda.synchronize()
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(full + 1)]
     end = torch.cuda.Event(enable_timing=True)
     marks[0].record()
@@ -105,6 +110,46 @@ def cpu_model():
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def pin_one_core():
+    """Pins this process to one CPU (the first it may use) for the CPU leg, as
+    `taskset -c` would; returns (that CPU, the previous set) or (None, None)."""
+    try:
+        allowed = os.sched_getaffinity(0)
+        core = min(allowed)
+        os.sched_setaffinity(0, {core})
+        return core, allowed
+    except (AttributeError, OSError):
+        return None, None
+
+
+def cpu_baseline_matmul(sizes, full_max=1024, sample_rows=16):
+    """The oracle's Tensor::matmul and Matmul VJP (tensor.rs:264-273, 424-444;
+    one thread) on config 2's inputs: forward + dA + dB in full for n <=
+    full_max; above, on the first `sample_rows` rows of A and G (C and dA
+    rows and their dB contributions, the same loops on fewer rows), the rate
+    scaled as FLOP done / time."""
+    import numpy as np
+
+    from katsu_amd import synth
+    from oracle import oracle as O
+    out = {}
+    for n in sizes:
+        rows = n if n <= full_max else min(n, sample_rows)
+        a = synth.uniform(synth.SEED_X, (n, n))[:rows]
+        b = synth.uniform(synth.SEED_W, (n, n))
+        g = np.ones((rows, n), np.float32)
+        t0 = time.perf_counter()
+        O.matmul(a, b)
+        O.matmul_vjp(a, b, g)
+        dt = time.perf_counter() - t0
+        flops = 3 * 2 * rows * n * n
+        out[str(n)] = {"tflops": round(flops / dt / 1e12, 6), "seconds": round(dt, 3),
+                       "sample": ("whole matrices" if rows == n else
+                                  f"{rows} of {n} rows of A and G (forward, dA rows, their "
+                                  f"dB terms): {flops / 1e9:.2f} GFLOP")}
+    return out
 
 
 def cpu_baseline(cfg, images, flops_per_image, outputs=None):
@@ -263,14 +308,19 @@ def main():
                   "bwd_data": ny + nw + nx, "bwd_filter": nx + ny + nw}
 
     torch.cuda.synchronize()
-    total_ms, spread = timed_steps(step, args.steps)
+    def poison():
+        for t in (yd, dxd, dwd):
+            t.fill_(float("nan"))
+
+    total_ms, spread = timed_steps(step, args.steps, reset=poison)
     ms_per_step = total_ms / args.steps
     step_med, step_iqr = med_iqr(spread)
-    # Every replay must reproduce the eager step bit for bit (the kernels are
+    # The outputs were NaN when the timed replays began: the replays wrote
+    # them, and must reproduce the eager step bit for bit (the kernels are
     # deterministic and the step overwrites its outputs).
     for got, ref, name in zip((yd, dxd, dwd), eager, ("y", "dx", "dw")):
         if not torch.equal(got, ref):
-            raise SystemExit(f"bench.py: graph replay of the step changed {name}")
+            raise SystemExit(f"bench.py: the timed replays of the step did not reproduce {name}")
 
     kernels = {}
     for name, g in g_pass.items():
@@ -408,8 +458,16 @@ def main():
 
     if not args.no_cpu:
         cpu_out = {}
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
-                                           step_flops / cfg["x"][0], cpu_out)
+        core, prev = pin_one_core()
+        try:
+            out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_images,
+                                               step_flops / cfg["x"][0], cpu_out)
+            if not args.no_matmul:
+                out["cpu_baseline"]["matmul"] = cpu_baseline_matmul(args.matmul_n)
+        finally:
+            if prev is not None:
+                os.sched_setaffinity(0, prev)
+        out["cpu_baseline"]["pinned_cpu"] = core
         if cpu_out:
             # The eager step's outputs used the same inputs and G.
             gpu_out = {"y": eager[0].cpu().numpy(), "dx": eager[1].cpu().numpy(),

@@ -22,9 +22,29 @@
  *     void*, 0 = the null stream) and return right after the launch.
  *
  * Threading: the reference engine is single-threaded (Rc handles,
- * tensor.rs:95-99).  Calls are serialised by an internal mutex, so the
- * library is safe to call from several threads, but the host-pointer entry
- * points share one stream and one staging pool.
+ * tensor.rs:95-99).  The library's host-side state is guarded by mutexes, so
+ * it is safe to call from several threads; the host-pointer entry points
+ * share one stream and one staging pool.
+ *
+ * Library scratch: the *_dev entry points that need device scratch (the dW
+ * split partials when no workspace is passed, the GEMM's split-K partials,
+ * the sum's chunk partials, Grad-CAM's channel weights) take it from one
+ * buffer per purpose that the library keeps and shares across all streams
+ * and graphs: an eager call sizes it, and a later capture of the same call
+ * on any stream uses it without allocating.  Calls (or graph replays) that
+ * overlap in time on different streams race on it; callers that run such
+ * calls concurrently order them, or pass their own workspace where the
+ * entry point takes one.  A buffer that must grow is replaced and the old
+ * block is kept (not freed) until katsu_hip_shutdown, so a graph captured
+ * earlier keeps valid addresses.
+ *
+ * Size limits: empty problems (an output with no elements, or an empty
+ * reduction) return KATSU_OK whatever their other dimensions.  Otherwise the
+ * kernels index in 32 bits and these entry points return KATSU_E_INVALID
+ * (launching nothing) when a bound is exceeded:
+ *   matmul:       m, n, k <= 2^31 - 1;
+ *   convolutions: C*H*W, K*OH*OW, K*C*R*S, N*H*W, N*OH*OW, pad, stride,
+ *                 H + 2*pad and W + 2*pad <= 2^31 - 1.
  */
 #ifndef KATSU_HIP_H
 #define KATSU_HIP_H
@@ -138,11 +158,13 @@ int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *
  * dx = beta*dx + dX and dw = beta*dw + dW, as the two calls above make them
  * (same results, same determinism).  When both passes take their direct
  * gfx950 kernels they share one launch, so dW work fills the GPU while the
- * last dX tiles finish.  dx and dw may be the same buffer (with beta = 1:
- * an engine's pending buffer when input and weights are one node); dX is
- * then added before dW, as the reference's adds are ordered
- * (tensor.rs:383-390).  The _dev form takes the workspace of
- * katsu_hip_conv2d_bwd_filter_workspace (or NULL, as above). */
+ * last dX tiles finish.  dx and dw may be the same buffer (an engine's
+ * pending buffer when input and weights are one node, so equal sizes): it
+ * then receives beta*buf + dX + dW, dX added first, as the reference's adds
+ * are ordered (tensor.rs:383-390).  Buffers that overlap without being the
+ * same are rejected with KATSU_E_INVALID.  The _dev form takes the
+ * workspace of katsu_hip_conv2d_bwd_filter_workspace (or NULL, as above),
+ * which covers this call as well as the filter gradient alone. */
 int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
                              float *dw, const katsu_conv_geom *g, float beta);
 int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy, float *dx,

@@ -3,6 +3,7 @@
 // repository root, crates/katsu-core/src/).
 #include "katsu.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <new>
 #include <stdexcept>
@@ -134,6 +135,20 @@ bool checked_mul(size_t a, size_t b, size_t *out) { return !__builtin_mul_overfl
 bool checked_add(size_t a, size_t b, size_t *out) { return !__builtin_add_overflow(a, b, out); }
 
 }  // namespace
+
+namespace testing {
+static std::atomic<int> publish_countdown{-1};
+void fail_publish_after(int n) { publish_countdown.store(n); }
+// True once the countdown set by fail_publish_after reaches zero.
+static bool publish_fault() {
+    int n = publish_countdown.load();
+    while (n >= 0) {
+        const int next = n == 0 ? -1 : n - 1;
+        if (publish_countdown.compare_exchange_weak(n, next)) return n == 0;
+    }
+    return false;
+}
+}  // namespace testing
 
 // tensor.rs:32-67.
 std::string TensorError::to_string() const {
@@ -488,16 +503,22 @@ struct Engine {
         }
         for (const Tensor &n : order)
             if (n.node_->borrows != 0) return err(TensorError::Kind::GradientBorrowed);
+        // All or nothing (tensor.rs:341-360): each new gradient is formed in
+        // the pass's own pending buffer (stored + pending, the same bits as
+        // the reference's `old += new`), and the stored gradients are replaced
+        // only once every launch has succeeded.
         for (const Tensor &n : order) {
+            const auto &stored = n.node_->grad;
+            if (!stored) continue;
             DeviceBuf &gradient = pending.at(n.node_.get()).buf;
-            auto &stored = n.node_->grad;
-            if (stored) {
-                const int rc =
-                    katsu_hip_accumulate_f32_dev(gradient.get(), stored->get(), n.numel(), 1.0f, st);
-                if (rc != KATSU_OK) return device(rc);
-            } else {
-                stored = std::move(gradient);
-            }
+            const int rc = testing::publish_fault()
+                               ? KATSU_E_LAUNCH
+                               : katsu_hip_accumulate_f32_dev(stored->get(), gradient.get(),
+                                                              n.numel(), 1.0f, st);
+            if (rc != KATSU_OK) return device(rc);
+        }
+        for (const Tensor &n : order) {
+            n.node_->grad = std::move(pending.at(n.node_.get()).buf);
             n.node_->grad_host_stale = true;
         }
         return Unit{};

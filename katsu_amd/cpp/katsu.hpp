@@ -228,4 +228,13 @@ Result<size_t> element_count(const std::vector<size_t> &shape);
 Result<Tensor> mean_pool_hw(const Tensor &y);
 Result<Tensor> spread_hw(const Tensor &dp, const std::vector<size_t> &shape);
 
+namespace testing {
+// Test support for the all-or-nothing publication of backward_with
+// (tensor.rs:341-360): the engine's publication step reports a failed device
+// call (TensorError::Device) after n more successful accumulation launches;
+// n < 0 (the default) never.  Forces the condition from the host, so no
+// kernel misbehaves.
+void fail_publish_after(int n);
+}  // namespace testing
+
 }  // namespace katsu

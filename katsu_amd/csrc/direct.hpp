@@ -30,6 +30,7 @@
 //   D: lane l, register v holds D[i = 4*(l/16) + v][j = l%16]
 #pragma once
 
+#include "exact.hpp"
 #include "igemm.hpp"
 
 namespace katsu {
@@ -587,38 +588,85 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
     const int np = p1 - p0;
-    if (EPI == 3) {
-        // Element e of a channel's run: super-pixel p0 + e/2, column phase e&1;
-        // consecutive lanes write consecutive pixels of a full-resolution row.
-        for (int row = wave; row < KT; row += 4) {
-            const int co = co0 + row;
-            if (co >= a.CO) break;
-            float *dst = outb + (int64_t)co * a.fh * a.fw;
-            for (int py = 0; py < 2; ++py)
-                for (int e = lane; e < 2 * np; e += 64) {
-                    const int p = p0 + (e >> 1), px = e & 1;
-                    const int Y = a.fd_ow.div(p);
-                    const int iy = 2 * Y + py, ix = 2 * (p - Y * a.OW) + px;
-                    if (iy < a.fh && ix < a.fw)
-                        store_beta(dst + iy * a.fw + ix,
-                                   ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], a.beta);
-                }
+    // A non-finite result is recomputed over the reference's visited products
+    // (exact.hpp) where the MFMA sum may hold a product the reference skips:
+    // an output whose window reaches the halo's padding (WMODE 0, 1, 3), or
+    // any output of the gathered super-filter (WMODE 2, whose absent taps are
+    // zeros multiplied by real G).  (oy, ox) is the output pixel of the
+    // kernel's own problem, (iy, ix) the full-resolution dX pixel of the
+    // stride-2 forms.
+    const float *in_img = a.in + (int64_t)n * a.in_img;
+    auto fix = [&](float v, int co, int oy, int ox, int iy, int ix) __attribute__((always_inline)) {
+        if (WMODE == 2) {
+            return exact_dx(in_img, a.w, a.CI, a.g_c, a.H, a.W, a.g_r, a.g_s, 2, a.g_pad,
+                            co >> 2, iy, ix);
         }
-    } else if (EPI == 1) {
-        for (int row = wave; row < KT; row += 4) {
-            const int co = co0 + row;
-            if (co >= a.CO) break;
-            const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
-            float *dst = outb + (int64_t)c * a.fh * a.fw;
-            for (int p = lane; p < np; p += 64) {
-                const int Y = a.fd_ow.div(p0 + p);
-                const int X = p0 + p - Y * a.OW;
-                const int iy = 2 * Y + py, ix = 2 * X + px;
-                if (iy < a.fh && ix < a.fw)
-                    store_beta(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], a.beta);
+        constexpr int WR = WMODE == 3 ? Dxs2Taps<R, S, PD>::DR : R;
+        constexpr int WS = WMODE == 3 ? Dxs2Taps<R, S, PD>::DS : S;
+        const int y0 = oy * a.st - a.pady, x0 = ox * a.st - a.padx;
+        if (y0 >= 0 && y0 + WR <= a.H && x0 >= 0 && x0 + WS <= a.W) return v;
+        if (WMODE == 0)
+            return exact_fwd(in_img, a.w, a.CI, a.H, a.W, R, S, a.st, a.pady, co, oy, ox);
+        if (WMODE == 1)
+            return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 1, R - 1 - a.pady, co, oy,
+                            ox);
+        return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 2, PD, co, iy, ix);
+    };
+    // Two passes over the block's outputs: the first stores every finite
+    // value and holds back the rest (so beta = 1 still adds to the original
+    // output); the second, entered only by a lane that held one back, stores
+    // the recomputed values.  The recomputation stays out of the stores'
+    // code, whose registers the MFMA loop sets.
+    // visit(dst, v, co, oy, ox, iy, ix) for every scalar output of the tile.
+    auto walk = [&](auto &&visit) __attribute__((always_inline)) {
+        if (EPI == 3) {
+            // Element e of a channel's run: super-pixel p0 + e/2, column phase
+            // e&1; consecutive lanes write consecutive pixels of a full-
+            // resolution row.
+            for (int row = wave; row < KT; row += 4) {
+                const int co = co0 + row;
+                if (co >= a.CO) break;
+                float *dst = outb + (int64_t)co * a.fh * a.fw;
+                for (int py = 0; py < 2; ++py)
+                    for (int e = lane; e < 2 * np; e += 64) {
+                        const int p = p0 + (e >> 1), px = e & 1;
+                        const int Y = a.fd_ow.div(p), X = p - Y * a.OW;
+                        const int iy = 2 * Y + py, ix = 2 * X + px;
+                        if (iy < a.fh && ix < a.fw)
+                            visit(dst + iy * a.fw + ix,
+                                  ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], co, Y,
+                                  X, iy, ix);
+                    }
+            }
+        } else if (EPI == 1) {
+            for (int row = wave; row < KT; row += 4) {
+                const int co = co0 + row;
+                if (co >= a.CO) break;
+                const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
+                float *dst = outb + (int64_t)c * a.fh * a.fw;
+                for (int p = lane; p < np; p += 64) {
+                    const int Y = a.fd_ow.div(p0 + p);
+                    const int X = p0 + p - Y * a.OW;
+                    const int iy = 2 * Y + py, ix = 2 * X + px;
+                    if (iy < a.fh && ix < a.fw)
+                        visit(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], co, Y, X, iy, ix);
+                }
+            }
+        } else {
+            for (int row = wave; row < KT; row += 4) {
+                const int co = co0 + row;
+                if (co >= a.CO) break;
+                float *dst = outb + (int64_t)co * a.OHW + p0;
+                for (int p = lane; p < np; p += 64) {
+                    const int oy = a.fd_ow.div(p0 + p);
+                    visit(dst + p, ys[row * Geo::YPITCH + p], co, oy, p0 + p - oy * a.OW, 0, 0);
+                }
             }
         }
-    } else if (a.out_vec) {
+    };
+    bool held = false;  // this lane held back a non-finite value
+    if (EPI == 0 && a.out_vec) {
+        // 16-byte runs: a run with a non-finite value is held back whole.
         const int n4 = np >> 2;
         for (int row = wave; row < KT; row += 4) {
             const int co = co0 + row;
@@ -626,19 +674,48 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             float *dst = outb + (int64_t)co * a.OHW + p0;
             for (int c4 = lane; c4 < n4; c4 += 64) {
                 floatx4 v = *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
+                if (!all_finite4(v[0], v[1], v[2], v[3])) {
+                    held = true;
+                    continue;
+                }
                 floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
                 if (a.beta != 0.f) v += *d;
                 *d = v;
             }
         }
-    } else {
-        for (int row = wave; row < KT; row += 4) {
-            const int co = co0 + row;
-            if (co >= a.CO) break;
-            float *dst = outb + (int64_t)co * a.OHW + p0;
-            for (int p = lane; p < np; p += 64)
-                store_beta(dst + p, ys[row * Geo::YPITCH + p], a.beta);
+        if (held) {
+            for (int row = wave; row < KT; row += 4) {
+                const int co = co0 + row;
+                if (co >= a.CO) break;
+                float *dst = outb + (int64_t)co * a.OHW + p0;
+                for (int c4 = lane; c4 < n4; c4 += 64) {
+                    floatx4 v =
+                        *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
+                    if (all_finite4(v[0], v[1], v[2], v[3])) continue;
+                    for (int q = 0; q < 4; ++q) {
+                        if (__builtin_isfinite(v[q])) continue;
+                        const int pp = p0 + c4 * 4 + q, oy = a.fd_ow.div(pp);
+                        v[q] = fix(v[q], co, oy, pp - oy * a.OW, 0, 0);
+                    }
+                    floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
+                    if (a.beta != 0.f) v += *d;
+                    *d = v;
+                }
+            }
         }
+    } else {
+        walk([&](float *dst, float v, int, int, int, int, int) __attribute__((always_inline)) {
+            if (__builtin_isfinite(v))
+                store_beta(dst, v, a.beta);
+            else
+                held = true;
+        });
+        if (held)
+            walk([&](float *dst, float v, int co, int oy, int ox, int iy, int ix)
+                     __attribute__((always_inline)) {
+                         if (!__builtin_isfinite(v))
+                             store_beta(dst, fix(v, co, oy, ox, iy, ix), a.beta);
+                     });
     }
 }
 
@@ -930,24 +1007,68 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
     __syncthreads();
     float *ob = a.out + (int64_t)split * a.split_stride;
     const int len = min(CT, a.C - c0) * RS;  // valid floats of a row
+    // A non-finite partial may hold a product the reference skips (a G value
+    // times the halo's padding, or a masked lane's zero times real x): it is
+    // recomputed over the block's output pixels, which are one contiguous
+    // range of the batch (exact.hpp).  As in the forward's epilogue, the
+    // first pass holds such values back and a second pass stores them.
+    auto fix = [&](int k, int e) __attribute__((always_inline)) {
+        const TileGeo g0 = geo(tb), g1 = geo(te - 1);
+        const int64_t pbeg = ((int64_t)g0.n * a.OH + g0.oy0) * a.OW + g0.cx0;
+        const int64_t pend = ((int64_t)g1.n * a.OH + g1.oy0 + g1.tr - 1) * a.OW + g1.cx1;
+        const int ce = e / RS, tap = e - (e / RS) * RS;
+        return exact_dw(a.x, a.g, a.C, a.H, a.W, a.K, a.OH, a.OW, a.st, a.pad, k, c0 + ce,
+                        tap / S, tap % S, pbeg, pend);
+    };
+    auto put = [&](float *dst, float v) __attribute__((always_inline)) {
+        if (a.split_stride == 0)
+            store_beta(dst, v, a.beta);
+        else
+            *dst = v;
+    };
+    bool held = false;
+    const bool vec = a.out_vec && len == CT * RS;
     for (int row = wave; row < KT; row += 4) {
         const int k = k0 + row;
         if (k >= a.K) break;
         float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
         const float *src = ps + row * Geo::PPITCH;
-        if (a.out_vec && len == CT * RS) {
+        if (vec) {
             for (int c4 = lane; c4 < CT * RS / 4; c4 += 64) {
                 floatx4 v = *reinterpret_cast<const floatx4 *>(src + c4 * 4);
+                if (!all_finite4(v[0], v[1], v[2], v[3])) {
+                    held = true;
+                    continue;
+                }
                 floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
                 if (a.split_stride == 0 && a.beta != 0.f) v += *d;
                 *d = v;
             }
         } else {
             for (int e = lane; e < len; e += 64) {
-                if (a.split_stride == 0)
-                    store_beta(dst + e, src[e], a.beta);
+                if (__builtin_isfinite(src[e]))
+                    put(dst + e, src[e]);
                 else
-                    dst[e] = src[e];
+                    held = true;
+            }
+        }
+    }
+    if (held) {
+        for (int row = wave; row < KT; row += 4) {
+            const int k = k0 + row;
+            if (k >= a.K) break;
+            float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
+            const float *src = ps + row * Geo::PPITCH;
+            for (int e = vec ? lane * 4 : lane; e < len; e += vec ? 256 : 64) {
+                // A held-back 16-byte run is written element by element.
+                const int ne = vec ? 4 : 1;
+                bool any = false;
+                for (int q = 0; q < ne; ++q) any |= !__builtin_isfinite(src[e + q]);
+                if (!any) continue;
+                for (int q = 0; q < ne; ++q) {
+                    const float v = src[e + q];
+                    put(dst + e + q, __builtin_isfinite(v) ? v : fix(k, e + q));
+                }
             }
         }
     }

@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "exact.hpp"
+
 namespace katsu {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -338,19 +340,28 @@ struct FwdColView {
     }
 };
 
-// Forward epilogue: C[i = oc][j = pixel] -> y[n][oc][oy][ox].
+// Forward epilogue: C[i = oc][j = pixel] -> y[n][oc][oy][ox].  A non-finite
+// sum may hold a weight times a padded zero, which the reference skips: it
+// is recomputed over the visited products (exact.hpp).
 struct FwdEpi {
     float *y;
     int K, OHW, npix;
     int64_t kohw;
     FastDiv fd_ohw;
-    struct JState { float *p; bool v; };
+    const float *x, *w;  // the operands, for the recomputation
+    int C, H, W, R, S, OW, stride, pad;
+    int64_t chw;
+    struct JState { float *p; int n, pix; bool v; };
     __device__ __forceinline__ JState prep_j(int j) const {
         const int n = fd_ohw.div(j);
-        return {y + (int64_t)n * kohw + (j - n * OHW), j < npix};
+        return {y + (int64_t)n * kohw + (j - n * OHW), n, j - n * OHW, j < npix};
     }
     __device__ __forceinline__ void store(const JState &s, int i, float v) const {
-        if (s.v && i < K) s.p[(int64_t)i * OHW] = v;
+        if (!(s.v && i < K)) return;
+        if (!__builtin_isfinite(v))
+            v = exact_fwd_inl(x + (int64_t)s.n * chw, w, C, H, W, R, S, stride, pad, i, s.pix / OW,
+                          s.pix % OW);
+        s.p[(int64_t)i * OHW] = v;
     }
 };
 
@@ -448,23 +459,33 @@ struct DxColView {
     }
 };
 
-// dX epilogue: C[i = c][j = (n,a,b)] -> dx[n][c][py+st*a][px+st*b].
+// dX epilogue: C[i = c][j = (n,a,b)] -> dx[n][c][py+st*a][px+st*b].  A
+// non-finite sum may hold a weight times a zero outside G, which the
+// reference skips: it is recomputed over the visited products (exact.hpp).
 struct DxEpi {
     float *dx;
     int C, HW, W, stride, py, px, Wa, HaWa, npix;
     int64_t chw;
     FastDiv fd_hawa, fd_wa;
     float beta;
-    struct JState { float *p; bool v; };
+    const float *g, *w;  // the operands, for the recomputation
+    int K, OH, OW, R, S, pad;
+    int64_t kohw;
+    struct JState { float *p; int n, iy, ix; bool v; };
     __device__ __forceinline__ JState prep_j(int j) const {
         const int n = fd_hawa.div(j);
         const int rem = j - n * HaWa;
         const int a = fd_wa.div(rem);
         const int b = rem - a * Wa;
-        return {dx + (int64_t)n * chw + (py + stride * a) * W + px + stride * b, j < npix};
+        const int iy = py + stride * a, ix = px + stride * b;
+        return {dx + (int64_t)n * chw + iy * W + ix, n, iy, ix, j < npix};
     }
     __device__ __forceinline__ void store(const JState &s, int i, float v) const {
-        if (s.v && i < C) store_beta(s.p + (int64_t)i * HW, v, beta);
+        if (!(s.v && i < C)) return;
+        if (!__builtin_isfinite(v))
+            v = exact_dx_inl(g + (int64_t)s.n * kohw, w, K, C, OH, OW, R, S, stride, pad, i, s.iy,
+                         s.ix);
+        store_beta(s.p + (int64_t)i * HW, v, beta);
     }
 };
 
@@ -578,19 +599,29 @@ struct DwColView {
 };
 
 // dW epilogue: C[i = oc][j = crs] -> out[split][oc][crs] (partials, beta 0)
-// or straight into dw with beta when there is a single split.
+// or straight into dw with beta when there is a single split.  A non-finite
+// partial may hold G times a padded zero, which the reference skips: it is
+// recomputed over the split's pixels [kbeg, kend) (exact.hpp).
 struct DwEpi {
     float *out;
     int K, CRS;
     int64_t split_stride;  // K*CRS, or 0 when writing dw directly
     float beta;
     int split;             // set per block
-    struct JState { float *p; bool v; };
+    const float *x, *g;    // the operands, for the recomputation
+    int C, H, W, OH, OW, R, S, stride, pad;
+    int kbeg, kend;        // set per block
+    struct JState { float *p; int j; bool v; };
     __device__ __forceinline__ JState prep_j(int j) const {
-        return {out + (int64_t)split * split_stride + j, j < CRS};
+        return {out + (int64_t)split * split_stride + j, j, j < CRS};
     }
     __device__ __forceinline__ void store(const JState &s, int i, float v) const {
-        if (s.v && i < K) store_beta(s.p + (int64_t)i * CRS, v, beta);
+        if (!(s.v && i < K)) return;
+        if (!__builtin_isfinite(v)) {
+            const int rs = R * S, c = s.j / rs, t = s.j - c * rs;
+            v = exact_dw_inl(x, g, C, H, W, K, OH, OW, stride, pad, i, c, t / S, t % S, kbeg, kend);
+        }
+        store_beta(s.p + (int64_t)i * CRS, v, beta);
     }
 };
 
@@ -614,6 +645,8 @@ struct DwProb {
         bp.kbeg = split * kchunk;
         bp.kend = min(npix, bp.kbeg + kchunk);
         ep.split = split;
+        ep.kbeg = bp.kbeg;
+        ep.kend = bp.kend;
     }
 };
 

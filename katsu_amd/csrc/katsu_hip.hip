@@ -15,6 +15,7 @@
 #include <map>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/katsu_hip.h"
 #include "igemm.hpp"
@@ -61,10 +62,6 @@ struct State {
     int device = -1;
     hipStream_t stream = nullptr;
     Buffer staging[5];
-    Buffer workspace;
-    Buffer sum_scratch;  // partial sums of katsu_hip_sum_f32_dev
-    Buffer cam_scratch;  // channel weights of katsu_hip_gradcam_f32_dev
-    Buffer gemm_ws;      // split-K partials of the GEMM
     Pool pool;
 };
 
@@ -78,6 +75,81 @@ int map_hip(hipError_t e) {
     if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return KATSU_E_OOM;
     if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) return KATSU_E_NODEVICE;
     return KATSU_E_LAUNCH;
+}
+
+// Library-owned scratch of the device entry points: the dW split partials
+// (when the caller passes no workspace), the GEMM's split-K partials, the
+// sum's chunk partials and Grad-CAM's channel weights, one buffer per
+// purpose.  The buffers are shared by every stream, so a call may run under
+// HIP graph capture on another stream than the eager call that sized them
+// (no allocation is then needed); calls that overlap in time on two streams
+// race on them.  A buffer that must grow is replaced, and the old block is
+// kept until katsu_hip_shutdown, because a graph captured earlier still
+// addresses it.  Its own mutex: the host-pointer entry points hold State::mu
+// while their device calls take scratch.
+enum class ScratchKind : int { Dw = 0, Gemm = 1, Sum = 2, Cam = 3, Count = 4 };
+
+struct ScratchPool {
+    std::mutex mu;
+    Buffer live[(int)ScratchKind::Count];
+    std::vector<void *> retired;
+};
+
+ScratchPool &scratch_pool() {
+    static ScratchPool p;
+    return p;
+}
+
+int scratch_get(ScratchKind kind, hipStream_t, size_t bytes, float **out) {
+    ScratchPool &p = scratch_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    Buffer &b = p.live[(int)kind];
+    if (b.bytes < bytes) {
+        void *ptr = nullptr;
+        const size_t want = std::max<size_t>(bytes, 256);
+        const hipError_t e = hipMalloc(&ptr, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return map_hip(e);
+        }
+        if (b.ptr) p.retired.push_back(b.ptr);
+        b.ptr = ptr;
+        b.bytes = want;
+    }
+    *out = (float *)b.ptr;
+    return KATSU_OK;
+}
+
+void scratch_release_all() {
+    ScratchPool &p = scratch_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    for (Buffer &b : p.live) {
+        if (b.ptr) (void)hipFree(b.ptr);
+        b = Buffer{};
+    }
+    for (void *q : p.retired) (void)hipFree(q);
+    p.retired.clear();
+}
+
+// Where a dW (or GEMM) launch takes its partial slices: the caller's
+// workspace when it passes one (checked against the plan), else the
+// library's scratch for the stream when `lib` allows it.
+struct WsSource {
+    void *ws = nullptr;
+    size_t bytes = 0;
+    bool lib = false;  // NULL workspace: use library scratch (else an error)
+};
+
+int ws_take(const WsSource &src, size_t need, hipStream_t st, float **out) {
+    *out = nullptr;
+    if (need == 0) return KATSU_OK;
+    if (src.ws) {
+        if (src.bytes < need) return KATSU_E_INVALID;
+        *out = (float *)src.ws;
+        return KATSU_OK;
+    }
+    if (!src.lib) return KATSU_E_INVALID;
+    return scratch_get(ScratchKind::Dw, st, need, out);
 }
 
 int init_locked(State &s) {
@@ -291,14 +363,10 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     if (!gemm_fast_plan(a, b, c, M, N, K, ta, tb, beta, &pl)) return false;
     GemmArgs g = pl.g;
     float *ws = nullptr;
-    if (pl.splits > 1) {
-        State &s = state();
-        std::lock_guard<std::mutex> lock(s.mu);
-        if ((*rc = ensure(s.gemm_ws, (size_t)(pl.splits * pl.pstride) * sizeof(float))) !=
-            KATSU_OK)
-            return true;
-        ws = (float *)s.gemm_ws.ptr;
-    }
+    if (pl.splits > 1 &&
+        (*rc = scratch_get(ScratchKind::Gemm, st, (size_t)(pl.splits * pl.pstride) * sizeof(float),
+                           &ws)) != KATSU_OK)
+        return true;
     g.c = pl.splits > 1 ? ws : c;
     g.split_stride = pl.splits > 1 ? pl.pstride : 0;
     // Fewer blocks than two per CU: two wave groups per block, so every SIMD
@@ -329,11 +397,18 @@ int gemm_vjp_launch(const GemmArgs &nt, const GemmArgs &tn, int64_t nb0, int64_t
 int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_t k, int ta,
              int tb, float beta, hipStream_t st) {
     if (!beta_ok(beta) || (ta != 0 && ta != 1) || (tb != 0 && tb != 1)) return KATSU_E_INVALID;
-    if ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max)
-        return KATSU_E_INVALID;
+    // Empty problems first, whatever their other dimensions (the reference
+    // accepts [usize::MAX, 0] . [0, 0], tests/tensor.rs:65-86).
     if (m == 0 || n == 0) return KATSU_OK;
     if (!c) return KATSU_E_INVALID;
-    if (k == 0) return launch_scale(c, (int64_t)m * (int64_t)n, beta, st);
+    if (k == 0) {
+        uint64_t mn;
+        if (__builtin_mul_overflow((uint64_t)m, (uint64_t)n, &mn) || mn > (uint64_t)INT64_MAX)
+            return KATSU_E_INVALID;
+        return launch_scale(c, (int64_t)mn, beta, st);
+    }
+    if ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max)
+        return KATSU_E_INVALID;
     if (!a || !b) return KATSU_E_INVALID;
     {
         int rc = KATSU_OK;
@@ -361,11 +436,15 @@ int gemm_dev(const float *a, const float *b, float *c, size_t m, size_t n, size_
 int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, float *db,
                    size_t m, size_t k, size_t n, float beta_a, float beta_b, hipStream_t st) {
     if (!beta_ok(beta_a) || !beta_ok(beta_b)) return KATSU_E_INVALID;
-    if ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max)
+    // An empty problem (C empty or k == 0, where the reference returns before
+    // either product, tensor.rs:421-423) goes to the two calls below, which
+    // write beta*da and beta*db and check nothing else.
+    const bool empty = m == 0 || n == 0 || k == 0;
+    if (!empty && ((int64_t)m > kI32Max || (int64_t)n > kI32Max || (int64_t)k > kI32Max))
         return KATSU_E_INVALID;
     const int64_t M = (int64_t)m, N = (int64_t)n, K = (int64_t)k;
     const bool apart = da && db && (da + M * K <= db || db + K * N <= da);
-    if (apart && M > 0 && N > 0 && K > 0 && a && b && g) {
+    if (apart && !empty && a && b && g) {
         GemmFastPlan pa, pb;
         if (gemm_fast_plan(g, b, da, M, K, N, 0, 1, beta_a, &pa) &&
             gemm_fast_plan(a, g, db, K, N, M, 1, 0, beta_b, &pb) && pa.T == pb.T &&
@@ -413,8 +492,23 @@ int geometry_fill(katsu_conv_geom *g) {
     if (__builtin_add_overflow(g->h, pad2, &ph) || __builtin_add_overflow(g->w, pad2, &pw))
         return KATSU_E_INVALID;
     if (ph < g->r || pw < g->s) return KATSU_E_INVALID;  // kernel exceeds padded input
-    g->oh = (ph - g->r) / g->stride + 1;
-    g->ow = (pw - g->s) / g->stride + 1;
+    const uint64_t oh = (ph - g->r) / g->stride + 1, ow = (pw - g->s) / g->stride + 1;
+    // element_count (tensor.rs:129-140) of C*H*W, K*OH*OW and N*K*OH*OW
+    // (conv2d.rs:196, 214-215): a product of non-zero dimensions must not
+    // overflow and must stay within isize::MAX / 4 floats.
+    auto count_ok = [](std::initializer_list<uint64_t> dims) {
+        uint64_t c = 1;
+        for (uint64_t v : dims) {
+            if (v == 0) return true;
+            if (!mul_ok(c, v, &c)) return false;
+        }
+        return c <= (uint64_t)INT64_MAX / sizeof(float);
+    };
+    if (!count_ok({g->c, g->h, g->w}) || !count_ok({g->k, oh, ow}) ||
+        !count_ok({g->n, g->k, oh, ow}))
+        return KATSU_E_INVALID;
+    g->oh = oh;
+    g->ow = ow;
     return KATSU_OK;
 }
 
@@ -1397,7 +1491,24 @@ int fwd_cfg(const float *x, const float *w, float *y, const ConvDims &d, hipStre
     b.fd_ow = fdiv(d.OW);
     b.fd_rs = fdiv(d.RS);
     b.fd_s = fdiv(d.S);
-    p.c = {y, d.K, d.OHW, (int)d.npix_out, (int64_t)d.KOHW, fdiv(d.OHW)};
+    FwdEpi &e = p.c;
+    e.y = y;
+    e.K = d.K;
+    e.OHW = d.OHW;
+    e.npix = (int)d.npix_out;
+    e.kohw = (int64_t)d.KOHW;
+    e.fd_ohw = fdiv(d.OHW);
+    e.x = x;
+    e.w = w;
+    e.C = d.C;
+    e.H = d.H;
+    e.W = d.W;
+    e.R = d.R;
+    e.S = d.S;
+    e.OW = d.OW;
+    e.stride = d.st;
+    e.pad = d.pad;
+    e.chw = d.CHW;
     p.CRS = d.CRS;
     p.tiles_m = (int)cdiv(d.K, C::BM);
     const int64_t tiles_n = cdiv(d.npix_out, C::BN);
@@ -1458,6 +1569,15 @@ int dx_cfg(const float *gy, const float *w, float *dx, const ConvDims &d, float 
     e.stride = d.st;
     e.chw = d.CHW;
     e.beta = beta;
+    e.g = gy;
+    e.w = w;
+    e.K = d.K;
+    e.OH = d.OH;
+    e.OW = d.OW;
+    e.R = d.R;
+    e.S = d.S;
+    e.pad = d.pad;
+    e.kohw = d.KOHW;
     p.tiles_m = (int)cdiv(d.C, C::BM);
 
     // Enumerate the stride phases; launch at most kMaxPhases per kernel.
@@ -1686,6 +1806,17 @@ int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float 
     p.c.split_stride = direct ? 0 : pl.pstride;
     p.c.beta = direct ? beta : 0.f;
     p.c.split = 0;
+    p.c.x = x;
+    p.c.g = gy;
+    p.c.C = d.C;
+    p.c.H = d.H;
+    p.c.W = d.W;
+    p.c.OH = d.OH;
+    p.c.OW = d.OW;
+    p.c.R = d.R;
+    p.c.S = d.S;
+    p.c.stride = d.st;
+    p.c.pad = d.pad;
     p.tiles_m = pl.tiles_m;
     p.tiles_n = pl.tiles_n;
     p.splits = pl.splits;
@@ -1697,8 +1828,7 @@ int dw_cfg(const float *x, const float *gy, float *dw, const ConvDims &d, float 
 }
 
 int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_conv_geom *g,
-                        float beta, void *ws, size_t ws_bytes, hipStream_t st,
-                        Buffer *fallback) {
+                        float beta, const WsSource &src, hipStream_t st) {
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     ConvDims d;
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
@@ -1706,17 +1836,9 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     if (d.npix_out == 0) return launch_scale(dw, (int64_t)d.K * d.CRS, beta, st);
     if (!x || !gy) return KATSU_E_INVALID;
     const DwPlan pl = dw_plan_any(d);
-    float *wsp = (float *)ws;
-    if (pl.ws_bytes > 0) {
-        if (!wsp) {
-            if (!fallback) return KATSU_E_INVALID;
-            int rc = ensure(*fallback, pl.ws_bytes);
-            if (rc != KATSU_OK) return rc;
-            wsp = (float *)fallback->ptr;
-        } else if (ws_bytes < pl.ws_bytes) {
-            return KATSU_E_INVALID;
-        }
-    }
+    float *wsp = nullptr;
+    int rc = ws_take(src, pl.ws_bytes, st, &wsp);
+    if (rc != KATSU_OK) return rc;
     if (pl.direct.ok) return direct_dw_launch(pl.direct, x, gy, dw, beta, wsp, st);
     if (pl.pw.ok) return pw_dw(x, gy, dw, d, pl.pw, beta, wsp, st);
     if (pl.stem.ok) return stem_dw_launch(pl.stem, x, gy, dw, beta, wsp, st);
@@ -1724,25 +1846,46 @@ int conv_bwd_filter_dev(const float *x, const float *gy, float *dw, const katsu_
     return dw_cfg<CfgW>(x, gy, dw, d, beta, wsp, st);
 }
 
+// The workspace that covers every path of the filter gradient and of the
+// one-call backward for this geometry (what the workspace query reports).
+size_t bwd_ws_bytes(const ConvDims &d) {
+    if (d.npix_out == 0) return 0;
+    size_t b = dw_plan_any(d).ws_bytes;
+    if (tiny_ok(d)) {
+        const TinyDwPlan tp = tiny_dw_plan(d);
+        if (tp.ok) b = std::max(b, tp.ws_bytes);
+    }
+    return b;
+}
+
 #ifndef KATSU_FUSED_DW_TBDIV
 #define KATSU_FUSED_DW_TBDIV 2
 #endif
 
+// Whether two buffers of na and nb floats share any byte.
+bool overlap(const float *a, size_t na, const float *b, size_t nb) {
+    if (!a || !b || na == 0 || nb == 0) return false;
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return a0 < b0 + nb * sizeof(float) && b0 < a0 + na * sizeof(float);
+}
+
 // Both backward passes (backward_buffers, conv2d.rs:265-292).  When dX and
 // dW both take their direct kernels they run as one launch; otherwise dX then
-// dW, as two.
+// dW, as two.  dx and dw either do not overlap or are the same buffer (an
+// engine's pending buffer when input and weights are one node: the two
+// passes then run one after the other, dX first).
 int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, float *dw,
-                 const katsu_conv_geom *g, float beta, void *ws, size_t ws_bytes, hipStream_t st,
-                 Buffer *fallback) {
+                 const katsu_conv_geom *g, float beta, const WsSource &src, hipStream_t st) {
     if (!beta_ok(beta)) return KATSU_E_INVALID;
     ConvDims d;
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
     if (!dw || (d.npix_in > 0 && !dx)) return KATSU_E_INVALID;
+    const size_t nx = (size_t)d.npix_in * d.C, nw = (size_t)d.K * d.CRS;
+    if (dx != dw && overlap(dx, nx, dw, nw)) return KATSU_E_INVALID;
+    if (dx == dw && nx != nw) return KATSU_E_INVALID;
     DirectFwdProblem P;
     DirectFwdPlan xp;
     DwPlan wpl;
-    // One output buffer for both (an engine's pending buffer when input and
-    // weights are one node): the two passes run one after the other.
     const bool xplan =
         d.st == 2 ? dx_phases_plan(d, gy, w, dx, beta, &xp)
                   : dx_as_forward(d, gy, w, dx, beta, &P) && P.CO >= FwdV::KT &&
@@ -1754,15 +1897,9 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
         // Few channels: dX rows and dW partials in one launch, then the reduce.
         const TinyDwPlan tp = tiny_dw_plan(d);
         if (tp.ok) {
-            float *wsp = (float *)ws;
-            if (!wsp) {
-                if (!fallback) return KATSU_E_INVALID;
-                const int rc = ensure(*fallback, tp.ws_bytes);
-                if (rc != KATSU_OK) return rc;
-                wsp = (float *)fallback->ptr;
-            } else if (ws_bytes < tp.ws_bytes) {
-                return KATSU_E_INVALID;
-            }
+            float *wsp = nullptr;
+            int rc = ws_take(src, tp.ws_bytes, st, &wsp);
+            if (rc != KATSU_OK) return rc;
             TinyArgs a = tiny_args(d);
             a.x = x;
             a.g = gy;
@@ -1776,8 +1913,7 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
             const size_t lds = std::max((size_t)tiny_dx_lds(d), tp.lds);
             tiny_bwd_kernel<<<dim3((unsigned)(ndx + tp.blocks)), dim3(256), lds, st>>>(a, w,
                                                                                       (int)ndx);
-            const int rc = launch_status();
-            if (rc != KATSU_OK) return rc;
+            if ((rc = launch_status()) != KATSU_OK) return rc;
             return launch_split_reduce(wsp, dw, (int64_t)d.K * d.CRS, tp.pstride, (int)tp.blocks,
                                        beta, st);
         }
@@ -1785,24 +1921,18 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
     if (!fused && dx != dw && d.npix_in > 0 && d.npix_out > 0 && x && w && gy && pw_ok(d)) {
         // 1x1: dX and the dW partials in one launch, then the reduce.
         const PwDwPlan pp = pw_dw_plan(d);
-        float *wsp = (float *)ws;
-        if (pp.ok && pp.ws_bytes > 0) {
-            if (!wsp) {
-                if (!fallback) return KATSU_E_INVALID;
-                const int rc = ensure(*fallback, pp.ws_bytes);
-                if (rc != KATSU_OK) return rc;
-                wsp = (float *)fallback->ptr;
-            } else if (ws_bytes < pp.ws_bytes) {
-                return KATSU_E_INVALID;
-            }
+        if (pp.ok) {
+            float *wsp = nullptr;
+            int rc = ws_take(src, pp.ws_bytes, st, &wsp);
+            if (rc != KATSU_OK) return rc;
+            if (pw_bwd(x, w, gy, dx, dw, d, pp, beta, wsp, st, &rc)) return rc;
         }
-        int rc = KATSU_OK;
-        if (pp.ok && pw_bwd(x, w, gy, dx, dw, d, pp, beta, wsp, st, &rc)) return rc;
     }
     if (!fused) {
+        // One buffer for both: it receives beta*buf + dX + dW, dX added first.
         const int rc = conv_bwd_data_dev(gy, w, dx, g, beta, st);
         if (rc != KATSU_OK) return rc;
-        return conv_bwd_filter_dev(x, gy, dw, g, beta, ws, ws_bytes, st, fallback);
+        return conv_bwd_filter_dev(x, gy, dw, g, dx == dw ? 1.f : beta, src, st);
     }
     // The shared launch takes the dW split with half the blocks: each dW
     // block then lasts about as long as two dX blocks, the dW blocks go
@@ -1811,17 +1941,9 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
     // workspace query reports.
     DirectDwPlan wp = direct_dw_plan_any(d, wpl.direct.variant, KATSU_FUSED_DW_TBDIV);
     if (!wp.ok || wp.ws_bytes > wpl.ws_bytes) wp = wpl.direct;
-    float *wsp = (float *)ws;
-    if (wp.ws_bytes > 0) {
-        if (!wsp) {
-            if (!fallback) return KATSU_E_INVALID;
-            const int rc = ensure(*fallback, wp.ws_bytes);
-            if (rc != KATSU_OK) return rc;
-            wsp = (float *)fallback->ptr;
-        } else if (ws_bytes < wpl.ws_bytes) {
-            return KATSU_E_INVALID;
-        }
-    }
+    float *wsp = nullptr;
+    const int rc = ws_take(src, wp.ws_bytes, st, &wsp);
+    if (rc != KATSU_OK) return rc;
     return bwd_fused_launch(xp, wp, x, gy, dw, beta, wsp, st);
 }
 
@@ -1939,14 +2061,8 @@ void katsu_hip_shutdown(void) {
         if (b.ptr) (void)hipFree(b.ptr);
         b = Buffer{};
     }
-    if (s.workspace.ptr) (void)hipFree(s.workspace.ptr);
-    s.workspace = Buffer{};
-    if (s.sum_scratch.ptr) (void)hipFree(s.sum_scratch.ptr);
-    s.sum_scratch = Buffer{};
-    if (s.cam_scratch.ptr) (void)hipFree(s.cam_scratch.ptr);
-    s.cam_scratch = Buffer{};
-    if (s.gemm_ws.ptr) (void)hipFree(s.gemm_ws.ptr);
-    s.gemm_ws = Buffer{};
+    (void)hipDeviceSynchronize();  // scratch may be in use on other streams
+    scratch_release_all();
     for (auto &kv : s.pool.free) (void)hipFree(kv.second);
     for (auto &kv : s.pool.live) (void)hipFree(kv.first);
     s.pool = Pool{};
@@ -2060,34 +2176,22 @@ int katsu_hip_conv2d_bwd_filter_workspace(const katsu_conv_geom *g, size_t *byte
     if (!bytes) return KATSU_E_INVALID;
     ConvDims d;
     if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
-    *bytes = d.npix_out == 0 ? 0 : dw_plan_any(d).ws_bytes;
+    *bytes = bwd_ws_bytes(d);
     return KATSU_OK;
 }
 
 int katsu_hip_conv2d_bwd_filter_f32_dev(const float *x, const float *gy, float *dw,
                                         const katsu_conv_geom *g, float beta, void *workspace,
                                         size_t workspace_bytes, void *stream) {
-    State &s = state();
-    if (workspace) {
-        return conv_bwd_filter_dev(x, gy, dw, g, beta, workspace, workspace_bytes,
-                                   (hipStream_t)stream, nullptr);
-    }
-    std::lock_guard<std::mutex> lock(s.mu);
-    return conv_bwd_filter_dev(x, gy, dw, g, beta, nullptr, 0, (hipStream_t)stream,
-                               &s.workspace);
+    return conv_bwd_filter_dev(x, gy, dw, g, beta, WsSource{workspace, workspace_bytes, true},
+                               (hipStream_t)stream);
 }
 
 int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy, float *dx,
                                  float *dw, const katsu_conv_geom *g, float beta, void *workspace,
                                  size_t workspace_bytes, void *stream) {
-    if (workspace) {
-        return conv_bwd_dev(x, w, gy, dx, dw, g, beta, workspace, workspace_bytes,
-                            (hipStream_t)stream, nullptr);
-    }
-    State &s = state();
-    std::lock_guard<std::mutex> lock(s.mu);
-    return conv_bwd_dev(x, w, gy, dx, dw, g, beta, nullptr, 0, (hipStream_t)stream,
-                        &s.workspace);
+    return conv_bwd_dev(x, w, gy, dx, dw, g, beta, WsSource{workspace, workspace_bytes, true},
+                        (hipStream_t)stream);
 }
 
 int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
@@ -2099,6 +2203,11 @@ int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, fl
                  ny = (size_t)d.npix_out * d.K;
     if (!dw || (nx > 0 && !dx)) return KATSU_E_INVALID;
     if (ny > 0 && (!x || !w || !gy)) return KATSU_E_INVALID;
+    // dx and dw: apart, or one buffer (one pending buffer for input and
+    // weights that are one node), which is staged once so the device passes
+    // see the aliasing and add dX before dW.
+    const bool same = dx == dw;
+    if ((same && nx != nw) || (!same && overlap(dx, nx, dw, nw))) return KATSU_E_INVALID;
     if (ny == 0) return host_scale(dw, nw, beta);  // empty batch: dx is empty, dw = beta*dw
     State &s = state();
     std::lock_guard<std::mutex> lock(s.mu);
@@ -2109,15 +2218,18 @@ int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, fl
     if ((rc = h2d(s.staging[2], gy, ny, s.stream))) return rc;
     if (beta != 0.f) {
         if ((rc = h2d(s.staging[3], dx, nx, s.stream))) return rc;
-        if ((rc = h2d(s.staging[4], dw, nw, s.stream))) return rc;
+        if (!same && (rc = h2d(s.staging[4], dw, nw, s.stream))) return rc;
     } else {
         if ((rc = ensure(s.staging[3], nx * sizeof(float)))) return rc;
-        if ((rc = ensure(s.staging[4], nw * sizeof(float)))) return rc;
+        if (!same && (rc = ensure(s.staging[4], nw * sizeof(float)))) return rc;
     }
+    float *ddx = (float *)s.staging[3].ptr;
+    float *ddw = same ? ddx : (float *)s.staging[4].ptr;
     rc = conv_bwd_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
-                      (const float *)s.staging[2].ptr, (float *)s.staging[3].ptr,
-                      (float *)s.staging[4].ptr, g, beta, nullptr, 0, s.stream, &s.workspace);
+                      (const float *)s.staging[2].ptr, ddx, ddw, g, beta,
+                      WsSource{nullptr, 0, true}, s.stream);
     if (rc) return rc;
+    if (same) return d2h_sync(dx, s.staging[3], nx, s.stream);
     if (nx > 0) {
         rc = map_hip(hipMemcpyAsync(dx, s.staging[3].ptr, nx * sizeof(float),
                                     hipMemcpyDeviceToHost, s.stream));
@@ -2148,8 +2260,8 @@ int katsu_hip_conv2d_bwd_filter_f32(const float *x, const float *gy, float *dw,
         return rc;
     }
     rc = conv_bwd_filter_dev((const float *)s.staging[0].ptr, (const float *)s.staging[1].ptr,
-                             (float *)s.staging[2].ptr, g, beta, nullptr, 0, s.stream,
-                             &s.workspace);
+                             (float *)s.staging[2].ptr, g, beta, WsSource{nullptr, 0, true},
+                             s.stream);
     if (rc) return rc;
     return d2h_sync(dw, s.staging[2], nw, s.stream);
 }
@@ -2262,13 +2374,10 @@ int katsu_hip_sum_f32_dev(const float *x, size_t n, float *out, float beta, void
     const int64_t N = (int64_t)n;
     const int64_t chunk = std::max<int64_t>(4096, cdiv(N, 1024));
     const int parts = (int)cdiv(N, chunk);
-    State &s = state();
-    float *part;
+    float *part = nullptr;
     {
-        std::lock_guard<std::mutex> lock(s.mu);
-        int rc = ensure(s.sum_scratch, (size_t)parts * sizeof(float));
+        const int rc = scratch_get(ScratchKind::Sum, st, (size_t)parts * sizeof(float), &part);
         if (rc) return rc;
-        part = (float *)s.sum_scratch.ptr;
     }
     if (chunk % 4 == 0 && aligned16(x))
         sum_partials<true><<<parts, 256, 0, st>>>(x, N, chunk, part);
@@ -2320,13 +2429,10 @@ int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, siz
     hipStream_t st = (hipStream_t)stream;
     const int64_t N = (int64_t)n, C = (int64_t)c, HW = (int64_t)hw;
     if (N > kI32Max) return KATSU_E_INVALID;
-    State &s = state();
-    float *alpha;
+    float *alpha = nullptr;
     {
-        std::lock_guard<std::mutex> lock(s.mu);
-        int rc = ensure(s.cam_scratch, (size_t)(N * C) * sizeof(float));
+        const int rc = scratch_get(ScratchKind::Cam, st, (size_t)(N * C) * sizeof(float), &alpha);
         if (rc) return rc;
-        alpha = (float *)s.cam_scratch.ptr;
     }
     if (HW % 4 == 0 && aligned16(grad))
         mean_rows<true><<<(unsigned)cdiv(N * C, 4), 256, 0, st>>>(grad, N * C, HW, alpha);

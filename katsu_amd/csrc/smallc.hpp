@@ -165,8 +165,13 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
         }
     };
     // Fragment f, register v: output channel 4*lg + v of the wave's 16,
-    // pixel 16f + l16 of the row.
+    // pixel 16f + l16 of the row.  A non-finite sum may hold a product the
+    // reference skips (the zero weight of tap s = 7 times real x, or a weight
+    // times the halo's padding): the lane notes it, and after the last row
+    // re-reads its own outputs and recomputes the non-finite ones over the
+    // visited products (exact.hpp), keeping that code out of the row loop.
     float *ybase = a.y + (int64_t)n * a.y_img;
+    bool held = false;
     auto store_row = [&](int oy) __attribute__((always_inline)) {
         if (oy < a.OH) {
 #pragma unroll
@@ -177,7 +182,10 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
 #pragma unroll
                 for (int f = 0; f < F; ++f) {
                     const int ox = f * 16 + l16;
-                    if (ox < a.OW) yrow[ox] = acc[f][v];
+                    if (ox < a.OW) {
+                        held |= !__builtin_isfinite(acc[f][v]);
+                        yrow[ox] = acc[f][v];
+                    }
                 }
             }
         }
@@ -204,6 +212,23 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
         wait_lds_dma();
         __syncthreads();
         store_row(oy + 2);
+    }
+    if (held) {
+        for (int t = 0; t < nsteps; ++t) {
+            const int oy = r0 + grp + 2 * t;
+            if (oy >= a.OH) break;
+            for (int v = 0; v < 4; ++v) {
+                const int co = co0 + wq * 16 + 4 * lg + v;
+                if (co >= a.K) continue;
+                float *yrow = ybase + ((int64_t)co * a.OH + oy) * a.OW;
+                for (int f = 0; f < F; ++f) {
+                    const int ox = f * 16 + l16;
+                    if (ox < a.OW && !__builtin_isfinite(yrow[ox]))
+                        yrow[ox] = exact_fwd_inl(a.x + (int64_t)n * a.x_img, a.w, a.C, a.H, a.W, R, S,
+                                             a.st, a.pad, co, oy, ox);
+                }
+            }
+        }
     }
 }
 
@@ -409,8 +434,21 @@ __global__ void __launch_bounds__(256, 2) stem_dw_kernel(const StemDwArgs a) {
     }
 
     // D layout: fragment (i, f), register v is channel wm*32 + 16i + 4lg + v,
-    // column 80wn + 16f + l16.
+    // column 80wn + 16f + l16.  A non-finite partial may hold a product the
+    // reference skips (G times the halo's padding, or a zeroed G column past
+    // the row end times real x): it is recomputed over the block's pixels,
+    // one contiguous range of the batch (exact.hpp).
     float *part = a.part + (int64_t)split * a.pstride;
+    auto fix = [&](float v, int o, int j) __attribute__((always_inline)) {
+        if (__builtin_isfinite(v) || tb >= te) return v;
+        const int rb = tb / a.tiles_row, re = (te - 1) / a.tiles_row;
+        const int64_t pbeg = (int64_t)rb * a.OW + (tb - rb * a.tiles_row) * TW;
+        const int64_t pend =
+            (int64_t)re * a.OW + min(((te - 1) - re * a.tiles_row) * TW + TW, a.OW);
+        const int c = j / (R * S), rs = j - c * (R * S);
+        return exact_dw_inl(a.x, a.g, a.C, a.H, a.W, a.K, a.OH, a.OW, ST, a.pad, o, c, rs / S, rs % S,
+                        pbeg, pend);
+    };
 #pragma unroll
     for (int f = 0; f < 5; ++f) {
         const int j = wn * 80 + f * 16 + l16;
@@ -420,7 +458,8 @@ __global__ void __launch_bounds__(256, 2) stem_dw_kernel(const StemDwArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int o = wm * 32 + i * 16 + 4 * lg + v;
-                if (co0 + o < a.K) part[(int64_t)(co0 + o) * Geo::NCOL + j] = acc[i][f][v];
+                if (co0 + o < a.K)
+                    part[(int64_t)(co0 + o) * Geo::NCOL + j] = fix(acc[i][f][v], co0 + o, j);
             }
     }
 }

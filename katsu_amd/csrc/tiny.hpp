@@ -247,10 +247,16 @@ __device__ __forceinline__ void tiny_dw_block(const TinyArgs &a, float *sm, int 
                    });
         wait_lds_dma();
         __syncthreads();
-        if (t < kcrs) {
+        if (t < kcrs && (unsigned)(iy0 + r) < (unsigned)a.H) {
+            // Only the pixels whose tap lies inside the image: the reference
+            // skips the others (conv2d.rs:240-255), so a non-finite G there
+            // never meets the padding's zeros.
+            const int gap = a.pad - s, span = a.W - 1 + a.pad - s;
+            const int lo = gap > 0 ? (gap + a.st - 1) / a.st : 0;
+            const int hi = span < 0 ? -1 : min(a.OW - 1, span / a.st);
             const float *gk = gs + k * a.OW;
             const float *xr = xs + (c * a.R + r) * a.xw + s;
-            for (int ox = 0; ox < a.OW; ++ox) acc += gk[ox] * xr[ox * a.st];
+            for (int ox = lo; ox <= hi; ++ox) acc += gk[ox] * xr[ox * a.st];
         }
         __syncthreads();
         if (++oy == a.OH) {

@@ -10,6 +10,8 @@
 // status is the number of failures.
 #include <cmath>
 #include <cstdio>
+#include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <limits>
@@ -427,6 +429,30 @@ void grad_cam_on_device() {
     }
 }
 
+// backward_with publishes all gradients or none (tensor.rs:341-360): a device
+// failure after the first node's accumulation leaves every stored gradient
+// as it was; the next pass accumulates into all of them.
+void publish_is_all_or_nothing() {
+    auto a = TRY(Tensor::create({1, 2, 3, 4}, {2, 2}));
+    auto b = TRY(Tensor::create({5, 6, 7, 8}, {2, 2}));
+    auto loss = TRY(TRY(a.matmul(b)).sum());
+    TRY(loss.backward());
+    const V ga = grad(a), gb = grad(b);
+    katsu::testing::fail_publish_after(1);
+    auto failed = loss.backward();
+    katsu::testing::fail_publish_after(-1);
+    CHECK(!failed.ok());
+    CHECK(failed.is(Kind::Device));
+    CHECK(grad(a) == ga);
+    CHECK(grad(b) == gb);
+    TRY(loss.backward());
+    V ga2(ga.size()), gb2(gb.size());
+    for (size_t i = 0; i < ga.size(); ++i) ga2[i] = 2 * ga[i];
+    for (size_t i = 0; i < gb.size(); ++i) gb2[i] = 2 * gb[i];
+    CHECK(grad(a) == ga2);  // small integers: exact
+    CHECK(grad(b) == gb2);
+}
+
 void known_stride_and_padding() {  // conv2d.rs:172-179
     auto x = TRY(Tensor::create(iota1(9), {1, 1, 3, 3}));
     auto layer = TRY(Conv2D::from_weights(TRY(Tensor::create({1, 2, 3, 4}, {1, 1, 2, 2})), 2, 1));
@@ -463,11 +489,33 @@ const Case kCases[] = {
     {"known_stride_and_padding", known_stride_and_padding},
     {"stem_chain_on_device", stem_chain_on_device},
     {"grad_cam_on_device", grad_cam_on_device},
+    {"publish_is_all_or_nothing", publish_is_all_or_nothing},
 };
 
 }  // namespace
 
+// `test_frontend --seeded-weights C K R S SEED`: the weights of
+// Conv2D::new_seeded(C, K, (R, S), 1, 0, SEED) as the hexadecimal bits of
+// each f32, one per line (host-side only: no device call).
+static int dump_seeded(char **argv) {
+    const size_t c = std::strtoull(argv[0], nullptr, 10), k = std::strtoull(argv[1], nullptr, 10),
+                 r = std::strtoull(argv[2], nullptr, 10), s = std::strtoull(argv[3], nullptr, 10);
+    const uint64_t seed = std::strtoull(argv[4], nullptr, 10);
+    auto layer = Conv2D::new_seeded(c, k, {r, s}, 1, 0, seed);
+    if (!layer.ok()) {
+        std::printf("ERROR %s\n", layer.error().to_string().c_str());
+        return 1;
+    }
+    for (float v : layer.value().weights().data()) {
+        uint32_t bits;
+        std::memcpy(&bits, &v, sizeof bits);
+        std::printf("%08x\n", bits);
+    }
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc == 7 && std::strcmp(argv[1], "--seeded-weights") == 0) return dump_seeded(argv + 2);
     int failures = 0;
     for (const Case &c : kCases) {
         if (argc > 1) {

@@ -69,6 +69,12 @@ def test_geometry_matches_reference(xs, ws, st, p):
     (1, 1, 2, 2, 1, 3, 3, 1, 0),      # kernel exceeds padded input
     (1, 1, 0, 2, 1, 1, 1, 1, 0),      # H = 0
     (0, 1, 2, 2, 1, 1, 1, 1, 2 ** 63),  # 2*pad overflows
+    # element_count (tensor.rs:129-140) of C*H*W, K*OH*OW, N*K*OH*OW
+    # (conv2d.rs:196, 214-215): overflow, or above isize::MAX / 4
+    (1, 2 ** 40, 2 ** 20, 2 ** 10, 1, 1, 1, 1, 0),
+    (1, 2 ** 31, 2 ** 30, 1, 1, 1, 1, 1, 0),
+    (1, 1, 1, 1, 2 ** 62, 1, 1, 1, 0),
+    (2 ** 31, 1, 1, 1, 2 ** 31, 1, 1, 1, 0),
 ])
 def test_geometry_rejects(args):
     with pytest.raises(katsu_amd.KatsuError) as e:
@@ -109,3 +115,50 @@ def test_empty_problems_need_no_device():
     w = np.ones((2, 3, 3, 3), np.float32)
     dx, dw = host.conv2d_backward(x, w, np.zeros((0, 2, 4, 5), np.float32), 1, 1)
     assert dx.size == 0 and np.all(dw == 0)
+
+
+def test_geometry_accepts_counts_at_the_limit():
+    """Products up to isize::MAX / 4 pass Geometry::new's checks (the 32-bit
+    kernel limits are the launchers' concern); batch 0 skips N*K*OH*OW."""
+    g = katsu_amd.geometry(1, 2 ** 30, 2 ** 29, 2, 1, 1, 1, 1, 0)  # C*H*W = 2^60
+    assert (g.oh, g.ow) == (2 ** 29, 2)
+    g = katsu_amd.geometry(0, 1, 1, 1, 2 ** 61 - 1, 1, 1, 1, 0)    # K*OH*OW = isize::MAX/4
+    assert (g.oh, g.ow) == (1, 1)
+    with pytest.raises(katsu_amd.KatsuError):
+        katsu_amd.geometry(0, 1, 1, 1, 2 ** 61, 1, 1, 1, 0)
+
+
+def test_empty_problems_before_size_limits():
+    """An empty matmul returns OK whatever its other dimensions, before the
+    32-bit limits (tests/tensor.rs:65-86 accepts [usize::MAX, 0] . [0, 0]),
+    on the host and device entry points and the VJP, with no device."""
+    L = katsu_amd.lib()
+    buf = (ctypes.c_float * 4)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    big = 2 ** 64 - 1
+    assert L.katsu_hip_gemm_f32(p, p, p, big, 0, 0, 0, 0, 0.0) == _abi.OK
+    assert L.katsu_hip_gemm_f32_dev(p, p, p, big, 0, 0, 0, 0, 0.0, None) == _abi.OK
+    assert L.katsu_hip_gemm_f32_dev(p, p, p, 0, 2 ** 40, 7, 0, 0, 1.0, None) == _abi.OK
+    assert L.katsu_hip_matmul_vjp_f32_dev(p, p, p, p, p, big, 0, 0, 1.0, 1.0, None) == _abi.OK
+    assert L.katsu_hip_matmul_vjp_f32_dev(p, p, p, p, p, 0, 5, 2 ** 40, 1.0, 1.0,
+                                          None) == _abi.OK
+    # Non-empty problems past the 32-bit limits are still refused.
+    assert L.katsu_hip_gemm_f32_dev(p, p, p, 2 ** 31, 4, 4, 0, 0, 0.0, None) == _abi.E_INVALID
+
+
+def test_overlapping_backward_outputs_are_rejected():
+    """dx and dw either apart or the same buffer: a partial overlap is
+    refused before anything is copied or launched (host and device forms)."""
+    L = katsu_amd.lib()
+    buf = np.zeros(200, np.float32)
+    base = buf.ctypes.data
+    g = katsu_amd.geometry(4, 3, 3, 3, 4, 3, 3, 1, 1)
+    x = ctypes.c_void_p(base)
+    # dx = buf[0:108], dw = buf[40:148]: they overlap without being equal.
+    dx, dw = ctypes.c_void_p(base), ctypes.c_void_p(base + 40 * 4)
+    assert L.katsu_hip_conv2d_bwd_f32(x, x, x, dx, dw, ctypes.byref(g), 1.0) == _abi.E_INVALID
+    assert L.katsu_hip_conv2d_bwd_f32_dev(x, x, x, dx, dw, ctypes.byref(g), 1.0, None, 0,
+                                          None) == _abi.E_INVALID
+    # The same buffer with different sizes cannot be one node's pending buffer.
+    g2 = katsu_amd.geometry(2, 3, 5, 5, 4, 3, 3, 1, 1)
+    assert L.katsu_hip_conv2d_bwd_f32(x, x, x, dx, dx, ctypes.byref(g2), 1.0) == _abi.E_INVALID

@@ -43,6 +43,7 @@ DEVICE = [
 EXTRA_DEVICE = [
     "stem_chain_on_device",
     "grad_cam_on_device",
+    "publish_is_all_or_nothing",
 ]
 
 
@@ -90,3 +91,27 @@ def test_frontend_host(name, host_results):
 def test_frontend_device(name, device_results):
     status, line = device_results.get(name, ("MISSING", name))
     assert status == "PASS", line
+
+
+def test_seeded_weights_match_repo_example():
+    """Conv2D::new_seeded(3, 8, (3, 3), 1, 1, 123), the repository example's
+    layer (examples/conv2d/main.rs:9), bit for bit against the weights the
+    oracle's restatement of conv2d.rs:35-61 wrote into
+    tests/golden/example_1b.json (host-side: no device call)."""
+    import json
+
+    import numpy as np
+    ref = json.load(open(os.path.join(ROOT, "tests", "golden", "example_1b.json")))["w"]
+    want = np.array(ref, np.float32).view(np.uint32)
+    proc = subprocess.run([_driver(), "--seeded-weights", "3", "8", "3", "3", "123"],
+                          capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    got = np.array([int(v, 16) for v in proc.stdout.split()], np.uint32)
+    assert got.shape == want.shape == (216,)
+    assert np.array_equal(got, want)
+    # And the oracle's own generator, on a second seed and shape.
+    proc = subprocess.run([_driver(), "--seeded-weights", "5", "4", "2", "3", "7"],
+                          capture_output=True, text=True, timeout=60)
+    got = np.array([int(v, 16) for v in proc.stdout.split()], np.uint32)
+    from oracle import oracle as O
+    assert np.array_equal(got, O.seeded_weights(5, 4, (2, 3), 7).ravel().view(np.uint32))

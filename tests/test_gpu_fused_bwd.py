@@ -120,3 +120,38 @@ def test_fused_host_entry_against_oracle():
     dxs, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
     assert_within(dx, dx_ref, dxs, 64 * 9, "fused host dX")
     assert_within(dw, dw_ref, dws, 16 * 24 * 24, "fused host dW")
+
+
+@pytest.mark.parametrize("name", ["c3_resnet", "c4a_down3x3"])
+def test_fused_full_size_sampled_exact(name, dev):
+    """The one-call backward the bench times, at the full BASELINE shape
+    (config 3: one direct_bwd_kernel launch of stride-1 dX and dW blocks;
+    config 4a: phase-form dX with stride-2 dW blocks), against exact f64 dot
+    products on sampled elements (corners and edges included).  The bound
+    2*gamma(K)*S takes S from the same f64 evaluation (tests/parity.py), not
+    from the GPU.  With the bench's all-ones G (config 3) and a random G."""
+    import torch
+
+    from katsu_amd import ops
+    from tests.parity import edge_samples, random_samples, sample_dw, sample_dx
+    c = synth.CONV_CONFIGS[name]
+    x, w = synth.conv_inputs(c)
+    st, p = c["stride"], c["pad"]
+    yshape = synth.out_shape(c)
+    k, cin, r, s = w.shape
+    kred_w = yshape[0] * yshape[2] * yshape[3]
+    grads = [synth.normal(synth.SEED_G, yshape)]
+    if name == "c3_resnet":
+        grads.append(np.ones(yshape, np.float32))
+    for g in grads:
+        xd, wd, gd = (torch.from_numpy(a).to(dev) for a in (x, w, g))
+        dx, dw = ops.conv2d_backward(xd, wd, gd, st, p)
+        torch.cuda.synchronize()
+        dx, dw = dx.cpu().numpy(), dw.cpu().numpy()
+        xs = random_samples(x.shape, 400, 5) + edge_samples(x.shape)
+        ref, sab = sample_dx(g, w, x.shape, st, p, xs)
+        assert_within(np.array([dx[t] for t in xs]), ref, sab, k * r * s, f"{name} dX")
+        ws = random_samples(w.shape, 96, 6) + [(0, 0, 0, 0), (k - 1, cin - 1, r - 1, s - 1),
+                                              (0, cin - 1, 0, s - 1), (k - 1, 0, r - 1, 0)]
+        ref, sab = sample_dw(x, g, w.shape, st, p, ws)
+        assert_within(np.array([dw[t] for t in ws]), ref, sab, kred_w, f"{name} dW")
