@@ -62,6 +62,7 @@ typedef enum katsu_status {
     KATSU_E_NODEVICE = 2, /* no HIP device, or device/runtime init failed */
     KATSU_E_OOM = 3,      /* device allocation failed */
     KATSU_E_LAUNCH = 4,   /* kernel launch, copy or synchronisation failed */
+    KATSU_E_SCRATCH = 5,  /* more scratch than the allocation-free entry point holds */
 } katsu_status;
 
 /* Convolution geometry, the fields of the reference's `struct Geometry`
@@ -170,6 +171,24 @@ int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, fl
 int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy, float *dx,
                                  float *dw, const katsu_conv_geom *g, float beta,
                                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* The one-call backward above with no allocation of any kind: no hipMalloc,
+ * hipFree or allocating library routine, on any call.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The dW
+ * split partials live in a static device array of
+ * katsu_hip_noalloc_scratch_bytes() bytes (40 MiB), one copy per GPU, held
+ * until the process ends; its address on a device is looked up on the first
+ * call there.  Same kernels, plans and results as
+ * katsu_hip_conv2d_bwd_f32_dev; a geometry whose partials would not fit
+ * returns KATSU_E_SCRATCH before any launch (no plan of this library needs
+ * more than 37.7 MB).  Every call on a GPU shares that GPU's array, so calls
+ * that overlap in time on one GPU (two streams, or two threads) race: the
+ * caller orders them. */
+int katsu_hip_conv2d_bwd_f32_dev_noalloc(const float *x, const float *w, const float *gy,
+                                         float *dx, float *dw, const katsu_conv_geom *g,
+                                         float beta, void *stream);
+size_t katsu_hip_noalloc_scratch_bytes(void);
 
 /* ---- Device residency and the engine's elementwise work -----------------
  * For callers that keep tensor data on the GPU between calls (a device

@@ -9,7 +9,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libkatsu_hip.so")
 
-OK, E_INVALID, E_NODEVICE, E_OOM, E_LAUNCH = 0, 1, 2, 3, 4
+OK, E_INVALID, E_NODEVICE, E_OOM, E_LAUNCH, E_SCRATCH = 0, 1, 2, 3, 4, 5
 
 # Every symbol include/katsu_hip.h declares.
 EXPORTS = (
@@ -21,6 +21,7 @@ EXPORTS = (
     "katsu_hip_conv2d_bwd_filter_workspace",
     "katsu_hip_conv2d_bwd_filter_f32", "katsu_hip_conv2d_bwd_filter_f32_dev",
     "katsu_hip_conv2d_bwd_f32", "katsu_hip_conv2d_bwd_f32_dev",
+    "katsu_hip_conv2d_bwd_f32_dev_noalloc", "katsu_hip_noalloc_scratch_bytes",
     "katsu_hip_stream", "katsu_hip_malloc", "katsu_hip_free", "katsu_hip_upload",
     "katsu_hip_download", "katsu_hip_sync",
     "katsu_hip_add_f32_dev", "katsu_hip_mul_f32_dev", "katsu_hip_accumulate_f32_dev",
@@ -75,6 +76,8 @@ def lib():
         L.katsu_hip_conv2d_bwd_filter_f32_dev.argtypes = [vp, vp, vp, gp, fp, vp, sz, vp]
         L.katsu_hip_conv2d_bwd_f32.argtypes = [vp, vp, vp, vp, vp, gp, fp]
         L.katsu_hip_conv2d_bwd_f32_dev.argtypes = [vp, vp, vp, vp, vp, gp, fp, vp, sz, vp]
+        L.katsu_hip_conv2d_bwd_f32_dev_noalloc.argtypes = [vp, vp, vp, vp, vp, gp, fp, vp]
+        L.katsu_hip_noalloc_scratch_bytes.argtypes = []
         L.katsu_hip_stream.restype = vp
         L.katsu_hip_stream.argtypes = []
         L.katsu_hip_malloc.argtypes = [ctypes.POINTER(vp), sz]
@@ -92,8 +95,10 @@ def lib():
         L.katsu_hip_broadcast_rows_f32_dev.argtypes = [vp, sz, sz, fp, vp, fp, vp]
         L.katsu_hip_gradcam_f32_dev.argtypes = [vp, vp, sz, sz, sz, vp, vp]
         for name in EXPORTS:
-            if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown"):
+            if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown",
+                            "katsu_hip_noalloc_scratch_bytes"):
                 getattr(L, name).restype = i
+        L.katsu_hip_noalloc_scratch_bytes.restype = sz
         _lib = L
     return _lib
 

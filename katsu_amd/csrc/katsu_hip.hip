@@ -1948,6 +1948,54 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
 }
 
 // ---------------------------------------------------------------------------
+// The allocation-free backward: its dW partials live in `scratch`, a
+// file-scope device array of which every GPU holds its own copy.  In host
+// code the array's name is only a stand-in, so its address on the current
+// device is looked up once per device (hipGetSymbolAddress) and that
+// pointer is what the kernels receive.  Every plan of this library needs at
+// most 37.7 MB of partials (about 512 blocks of one 64 x 288 tile each),
+// which the array covers.  Calls on one GPU share it: calls that overlap in
+// time on that GPU race.  Nothing in it needs to start at zero (every
+// partial element the reduce reads is written first).
+
+constexpr size_t kStaticScratchBytes = (size_t)40 << 20;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+
+struct StaticScratch {
+    std::mutex mu;
+    void *ptr[kMaxDevices] = {};
+};
+
+StaticScratch &static_scratch_state() {
+    static StaticScratch s;
+    return s;
+}
+
+// This device's copy of `scratch` (set up on the first call per device).
+int static_scratch(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return KATSU_E_NODEVICE;
+    }
+    StaticScratch &s = static_scratch_state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (!s.ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return e == hipSuccess ? KATSU_E_LAUNCH : map_hip(e);
+        }
+        s.ptr[dev] = p;
+    }
+    *out = s.ptr[dev];
+    return KATSU_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Device engine: buffers and the elementwise kernels.
 
 // Pool block sizes: 512-byte granules below 1 MiB, 2 MiB granules above.
@@ -2042,6 +2090,8 @@ const char *katsu_hip_strerror(int status) {
         case KATSU_E_NODEVICE: return "no HIP device available";
         case KATSU_E_OOM: return "device allocation failed";
         case KATSU_E_LAUNCH: return "kernel launch, copy or synchronisation failed";
+        case KATSU_E_SCRATCH:
+            return "the problem needs more scratch than the allocation-free entry point holds";
         default: return "unknown katsu status";
     }
 }
@@ -2193,6 +2243,22 @@ int katsu_hip_conv2d_bwd_f32_dev(const float *x, const float *w, const float *gy
     return conv_bwd_dev(x, w, gy, dx, dw, g, beta, WsSource{workspace, workspace_bytes, true},
                         (hipStream_t)stream);
 }
+
+int katsu_hip_conv2d_bwd_f32_dev_noalloc(const float *x, const float *w, const float *gy,
+                                         float *dx, float *dw, const katsu_conv_geom *g,
+                                         float beta, void *stream) {
+    if (!beta_ok(beta)) return KATSU_E_INVALID;
+    ConvDims d;
+    if (conv_dims(g, &d) != KATSU_OK) return KATSU_E_INVALID;
+    if (bwd_ws_bytes(d) > kStaticScratchBytes) return KATSU_E_SCRATCH;
+    void *ws = nullptr;
+    const int rc = static_scratch(&ws);
+    if (rc != KATSU_OK) return rc;
+    return conv_bwd_dev(x, w, gy, dx, dw, g, beta, WsSource{ws, kStaticScratchBytes, false},
+                        (hipStream_t)stream);
+}
+
+size_t katsu_hip_noalloc_scratch_bytes(void) { return kStaticScratchBytes; }
 
 int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
                              float *dw, const katsu_conv_geom *g, float beta) {

@@ -38,7 +38,7 @@ def test_library_is_gfx950_build():
 
 def test_strerror_texts():
     assert katsu_amd.strerror(0) == "ok"
-    for code in (1, 2, 3, 4):
+    for code in (1, 2, 3, 4, 5):
         assert katsu_amd.strerror(code) != "unknown katsu status"
     assert katsu_amd.strerror(99) == "unknown katsu status"
 
