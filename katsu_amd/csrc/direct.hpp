@@ -221,7 +221,9 @@ struct DirectFwdGeo {
     static constexpr int YPITCH = TPMAX + 4;
     static constexpr int NPH = WMODE == 3 ? 4 : 1;  // accumulator sets (phases)
     static_assert(NPH * KT * YPITCH <= 2 * STAGE, "output tile must fit the LDS stages");
-    static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
+    // One word past the stages: the block's flag for a non-finite result.
+    static constexpr int FLAG = 2 * STAGE;
+    static constexpr size_t kBytes = (2 * (size_t)STAGE + 4) * sizeof(float);
     // WMODE 2 weight slots per lane (4-byte wave loads spread over 4 waves).
     static constexpr int WSLOTS = (WS / 64 + 3) / 4;
 };
@@ -240,6 +242,73 @@ struct DirectFwdGeo {
 // 16 consecutive pixels would wrap onto the next row, whose lanes then share
 // LDS banks with the first row's; one row per fragment keeps the 16 lanes on
 // 16 consecutive floats.  Tiles are whole rows.
+// The epilogue of a forward-shaped block that holds a non-finite sum: every
+// output is stored as in the fast epilogue, except that a non-finite one is
+// first recomputed over the reference's visited products (exact.hpp) where
+// the MFMA sum may hold a product the reference skips: an output whose
+// window reaches the halo's padding (WMODE 0, 1, 3), or any output of the
+// gathered super-filter (WMODE 2, whose absent taps are zeros multiplied by
+// real G).  (oy, ox) is the output pixel of the kernel's own problem, (iy,
+// ix) the full-resolution dX pixel of the stride-2 forms.  Taken only for
+// non-finite data, so it is written for clarity, not speed.
+template <int KT, int R, int S, int WMODE, int EPI, int PD>
+__device__ __forceinline__ void direct_fwd_epilogue_exact(const DirectArgs &a, const float *ys,
+                                                       int ypitch, float *outb, int n, int p0,
+                                                       int np, int co0, int wave, int lane) {
+    const float *in_img = a.in + (int64_t)n * a.in_img;
+    auto fix = [&](float v, int co, int oy, int ox, int iy, int ix) {
+        if (__builtin_isfinite(v)) return v;
+        if (WMODE == 2)
+            return exact_dx(in_img, a.w, a.CI, a.g_c, a.H, a.W, a.g_r, a.g_s, 2, a.g_pad,
+                            co >> 2, iy, ix);
+        constexpr int WR = WMODE == 3 ? Dxs2Taps<R, S, PD>::DR : R;
+        constexpr int WS = WMODE == 3 ? Dxs2Taps<R, S, PD>::DS : S;
+        const int y0 = oy * a.st - a.pady, x0 = ox * a.st - a.padx;
+        if (y0 >= 0 && y0 + WR <= a.H && x0 >= 0 && x0 + WS <= a.W) return v;
+        if (WMODE == 0)
+            return exact_fwd(in_img, a.w, a.CI, a.H, a.W, R, S, a.st, a.pady, co, oy, ox);
+        if (WMODE == 1)
+            return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 1, R - 1 - a.pady, co, oy,
+                            ox);
+        return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 2, PD, co, iy, ix);
+    };
+    for (int row = wave; row < KT; row += 4) {
+        const int co = co0 + row;
+        if (co >= a.CO) break;
+        if (EPI == 3) {
+            float *dst = outb + (int64_t)co * a.fh * a.fw;
+            for (int py = 0; py < 2; ++py)
+                for (int e = lane; e < 2 * np; e += 64) {
+                    const int p = p0 + (e >> 1), px = e & 1;
+                    const int Y = a.fd_ow.div(p), X = p - Y * a.OW;
+                    const int iy = 2 * Y + py, ix = 2 * X + px;
+                    if (iy < a.fh && ix < a.fw)
+                        store_beta(dst + iy * a.fw + ix,
+                                   fix(ys[((2 * py + px) * KT + row) * ypitch + (e >> 1)], co, Y,
+                                       X, iy, ix),
+                                   a.beta);
+                }
+        } else if (EPI == 1) {
+            const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
+            float *dst = outb + (int64_t)c * a.fh * a.fw;
+            for (int p = lane; p < np; p += 64) {
+                const int Y = a.fd_ow.div(p0 + p), X = p0 + p - Y * a.OW;
+                const int iy = 2 * Y + py, ix = 2 * X + px;
+                if (iy < a.fh && ix < a.fw)
+                    store_beta(dst + iy * a.fw + ix, fix(ys[row * ypitch + p], co, Y, X, iy, ix),
+                               a.beta);
+            }
+        } else {
+            float *dst = outb + (int64_t)co * a.OHW + p0;
+            for (int p = lane; p < np; p += 64) {
+                const int oy = a.fd_ow.div(p0 + p);
+                store_beta(dst + p, fix(ys[row * ypitch + p], co, oy, p0 + p - oy * a.OW, 0, 0),
+                           a.beta);
+            }
+        }
+    }
+}
+
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
           bool WVEC, bool S2 = false, bool RF = false, int PD = 0>
 __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
@@ -540,6 +609,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     const int nch = (a.CI + CB - 1) / CB;
     float *st0 = smem;
     float *st1 = smem + Geo::STAGE;
+    if (tid == 0) smem[Geo::FLAG] = 0.f;  // published by the barriers below
     stage_in(st0, 0);
     wait_lds_dma();
     __syncthreads();
@@ -580,6 +650,24 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                        (lane & 15)] = ac[f][v];
         }
     };
+    // A non-finite sum may hold a product the reference skips: the block
+    // notes whether any of its sums is non-finite (a test of the
+    // accumulators, before they go through LDS) in one LDS word, and only a
+    // block that has one takes the epilogue that recomputes them; the others
+    // store as fast as they would without the test.
+    {
+        bool bad = false;
+#pragma unroll
+        for (int f = 0; f < F; ++f) bad |= !all_finite4(acc[f][0], acc[f][1], acc[f][2], acc[f][3]);
+        if (WMODE == 3) {
+#pragma unroll
+            for (int p = 0; p < (WMODE == 3 ? 3 : 1); ++p)
+#pragma unroll
+                for (int f = 0; f < F; ++f)
+                    bad |= !all_finite4(acc3[p][f][0], acc3[p][f][1], acc3[p][f][2], acc3[p][f][3]);
+        }
+        if (bad) smem[Geo::FLAG] = 1.f;
+    }
     put(0, acc);
     if (WMODE == 3) {
 #pragma unroll
@@ -588,85 +676,43 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
     const int np = p1 - p0;
-    // A non-finite result is recomputed over the reference's visited products
-    // (exact.hpp) where the MFMA sum may hold a product the reference skips:
-    // an output whose window reaches the halo's padding (WMODE 0, 1, 3), or
-    // any output of the gathered super-filter (WMODE 2, whose absent taps are
-    // zeros multiplied by real G).  (oy, ox) is the output pixel of the
-    // kernel's own problem, (iy, ix) the full-resolution dX pixel of the
-    // stride-2 forms.
-    const float *in_img = a.in + (int64_t)n * a.in_img;
-    auto fix = [&](float v, int co, int oy, int ox, int iy, int ix) __attribute__((always_inline)) {
-        if (WMODE == 2) {
-            return exact_dx(in_img, a.w, a.CI, a.g_c, a.H, a.W, a.g_r, a.g_s, 2, a.g_pad,
-                            co >> 2, iy, ix);
-        }
-        constexpr int WR = WMODE == 3 ? Dxs2Taps<R, S, PD>::DR : R;
-        constexpr int WS = WMODE == 3 ? Dxs2Taps<R, S, PD>::DS : S;
-        const int y0 = oy * a.st - a.pady, x0 = ox * a.st - a.padx;
-        if (y0 >= 0 && y0 + WR <= a.H && x0 >= 0 && x0 + WS <= a.W) return v;
-        if (WMODE == 0)
-            return exact_fwd(in_img, a.w, a.CI, a.H, a.W, R, S, a.st, a.pady, co, oy, ox);
-        if (WMODE == 1)
-            return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 1, R - 1 - a.pady, co, oy,
-                            ox);
-        return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 2, PD, co, iy, ix);
-    };
-    // Two passes over the block's outputs: the first stores every finite
-    // value and holds back the rest (so beta = 1 still adds to the original
-    // output); the second, entered only by a lane that held one back, stores
-    // the recomputed values.  The recomputation stays out of the stores'
-    // code, whose registers the MFMA loop sets.
-    // visit(dst, v, co, oy, ox, iy, ix) for every scalar output of the tile.
-    auto walk = [&](auto &&visit) __attribute__((always_inline)) {
-        if (EPI == 3) {
-            // Element e of a channel's run: super-pixel p0 + e/2, column phase
-            // e&1; consecutive lanes write consecutive pixels of a full-
-            // resolution row.
-            for (int row = wave; row < KT; row += 4) {
-                const int co = co0 + row;
-                if (co >= a.CO) break;
-                float *dst = outb + (int64_t)co * a.fh * a.fw;
-                for (int py = 0; py < 2; ++py)
-                    for (int e = lane; e < 2 * np; e += 64) {
-                        const int p = p0 + (e >> 1), px = e & 1;
-                        const int Y = a.fd_ow.div(p), X = p - Y * a.OW;
-                        const int iy = 2 * Y + py, ix = 2 * X + px;
-                        if (iy < a.fh && ix < a.fw)
-                            visit(dst + iy * a.fw + ix,
-                                  ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], co, Y,
-                                  X, iy, ix);
-                    }
-            }
-        } else if (EPI == 1) {
-            for (int row = wave; row < KT; row += 4) {
-                const int co = co0 + row;
-                if (co >= a.CO) break;
-                const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
-                float *dst = outb + (int64_t)c * a.fh * a.fw;
-                for (int p = lane; p < np; p += 64) {
-                    const int Y = a.fd_ow.div(p0 + p);
-                    const int X = p0 + p - Y * a.OW;
-                    const int iy = 2 * Y + py, ix = 2 * X + px;
+    if (smem[Geo::FLAG] != 0.f) {
+        direct_fwd_epilogue_exact<KT, R, S, WMODE, EPI, PD>(a, ys, Geo::YPITCH, outb, n, p0, np,
+                                                            co0, wave, lane);
+        return;
+    }
+    if (EPI == 3) {
+        // Element e of a channel's run: super-pixel p0 + e/2, column phase e&1;
+        // consecutive lanes write consecutive pixels of a full-resolution row.
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            float *dst = outb + (int64_t)co * a.fh * a.fw;
+            for (int py = 0; py < 2; ++py)
+                for (int e = lane; e < 2 * np; e += 64) {
+                    const int p = p0 + (e >> 1), px = e & 1;
+                    const int Y = a.fd_ow.div(p);
+                    const int iy = 2 * Y + py, ix = 2 * (p - Y * a.OW) + px;
                     if (iy < a.fh && ix < a.fw)
-                        visit(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], co, Y, X, iy, ix);
+                        store_beta(dst + iy * a.fw + ix,
+                                   ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], a.beta);
                 }
-            }
-        } else {
-            for (int row = wave; row < KT; row += 4) {
-                const int co = co0 + row;
-                if (co >= a.CO) break;
-                float *dst = outb + (int64_t)co * a.OHW + p0;
-                for (int p = lane; p < np; p += 64) {
-                    const int oy = a.fd_ow.div(p0 + p);
-                    visit(dst + p, ys[row * Geo::YPITCH + p], co, oy, p0 + p - oy * a.OW, 0, 0);
-                }
+        }
+    } else if (EPI == 1) {
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
+            float *dst = outb + (int64_t)c * a.fh * a.fw;
+            for (int p = lane; p < np; p += 64) {
+                const int Y = a.fd_ow.div(p0 + p);
+                const int X = p0 + p - Y * a.OW;
+                const int iy = 2 * Y + py, ix = 2 * X + px;
+                if (iy < a.fh && ix < a.fw)
+                    store_beta(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], a.beta);
             }
         }
-    };
-    bool held = false;  // this lane held back a non-finite value
-    if (EPI == 0 && a.out_vec) {
-        // 16-byte runs: a run with a non-finite value is held back whole.
+    } else if (a.out_vec) {
         const int n4 = np >> 2;
         for (int row = wave; row < KT; row += 4) {
             const int co = co0 + row;
@@ -674,48 +720,19 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             float *dst = outb + (int64_t)co * a.OHW + p0;
             for (int c4 = lane; c4 < n4; c4 += 64) {
                 floatx4 v = *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
-                if (!all_finite4(v[0], v[1], v[2], v[3])) {
-                    held = true;
-                    continue;
-                }
                 floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
                 if (a.beta != 0.f) v += *d;
                 *d = v;
             }
         }
-        if (held) {
-            for (int row = wave; row < KT; row += 4) {
-                const int co = co0 + row;
-                if (co >= a.CO) break;
-                float *dst = outb + (int64_t)co * a.OHW + p0;
-                for (int c4 = lane; c4 < n4; c4 += 64) {
-                    floatx4 v =
-                        *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
-                    if (all_finite4(v[0], v[1], v[2], v[3])) continue;
-                    for (int q = 0; q < 4; ++q) {
-                        if (__builtin_isfinite(v[q])) continue;
-                        const int pp = p0 + c4 * 4 + q, oy = a.fd_ow.div(pp);
-                        v[q] = fix(v[q], co, oy, pp - oy * a.OW, 0, 0);
-                    }
-                    floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
-                    if (a.beta != 0.f) v += *d;
-                    *d = v;
-                }
-            }
-        }
     } else {
-        walk([&](float *dst, float v, int, int, int, int, int) __attribute__((always_inline)) {
-            if (__builtin_isfinite(v))
-                store_beta(dst, v, a.beta);
-            else
-                held = true;
-        });
-        if (held)
-            walk([&](float *dst, float v, int co, int oy, int ox, int iy, int ix)
-                     __attribute__((always_inline)) {
-                         if (!__builtin_isfinite(v))
-                             store_beta(dst, fix(v, co, oy, ox, iy, ix), a.beta);
-                     });
+        for (int row = wave; row < KT; row += 4) {
+            const int co = co0 + row;
+            if (co >= a.CO) break;
+            float *dst = outb + (int64_t)co * a.OHW + p0;
+            for (int p = lane; p < np; p += 64)
+                store_beta(dst + p, ys[row * Geo::YPITCH + p], a.beta);
+        }
     }
 }
 
@@ -760,6 +777,7 @@ struct DirectDwArgs {
     int64_t split_stride;  // floats between partials, or 0 when writing dw directly
     float beta;            // applied only when writing dw directly
     FastDiv fd_tiles_img, fd_segs;
+    int flag;              // LDS float index of the block's non-finite flag (past the stages)
 };
 
 // Compile-time part of the dW LDS layout; the G tile's pitch is chosen per
@@ -780,6 +798,34 @@ struct DirectDwGeo {
 // (16*WKF) oc x 16 c x R*S taps; each k-step reads WKF A and R*S B
 // fragments for WKF*R*S MFMAs.  FULL: every tile row is a multiple of 4
 // pixels wide, so no k-step holds a pixel past the end of its row.
+// The epilogue of a dW block that holds a non-finite partial: every element
+// is stored as in the fast epilogue, except that a non-finite one is first
+// recomputed over the block's output pixels [pbeg, pend) (exact.hpp).  Taken
+// only for non-finite data.
+template <int KT, int RS, int S>
+__device__ __forceinline__ void direct_dw_epilogue_exact(const DirectDwArgs &a, const float *ps,
+                                                      int ppitch, float *ob, int k0, int c0,
+                                                      int len, int64_t pbeg, int64_t pend,
+                                                      int wave, int lane) {
+    for (int row = wave; row < KT; row += 4) {
+        const int k = k0 + row;
+        if (k >= a.K) break;
+        float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
+        for (int e = lane; e < len; e += 64) {
+            float v = ps[row * ppitch + e];
+            if (!__builtin_isfinite(v)) {
+                const int ce = e / RS, tap = e - (e / RS) * RS;
+                v = exact_dw(a.x, a.g, a.C, a.H, a.W, a.K, a.OH, a.OW, a.st, a.pad, k, c0 + ce,
+                             tap / S, tap % S, pbeg, pend);
+            }
+            if (a.split_stride == 0)
+                store_beta(dst + e, v, a.beta);
+            else
+                dst[e] = v;
+        }
+    }
+}
+
 template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
 __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, int nb) {
     using Geo = DirectDwGeo<KT, CT, R, S, ROWS, PITCH, GPC>;
@@ -963,6 +1009,9 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
             run(fetch, nsteps);
         }
     };
+    // Cleared before the stage loop's barriers; a block without tiles has
+    // zero sums and never sets it.
+    if (tid == 0) smem[a.flag] = 0.f;
     if (tb < te) {
         float *st0 = smem;
         float *st1 = smem + a.stage;
@@ -994,8 +1043,21 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
 
     // Epilogue: D[i = oc][j = c] per tap, transposed through LDS into the
     // partial's row order [oc][c][tap], then written as contiguous runs of
-    // CT*RS floats per output channel.
+    // CT*RS floats per output channel.  A non-finite partial may hold a
+    // product the reference skips (a G value times the halo's padding, or a
+    // masked lane's zero times real x): as in the forward's epilogue, the
+    // block notes one in an LDS word (the accumulators are tested before the
+    // transpose), and only then takes the epilogue that recomputes them.
     float *ps = smem;
+    {
+        bool bad = false;
+#pragma unroll
+        for (int f = 0; f < WKF; ++f)
+#pragma unroll
+            for (int tap = 0; tap < RS; ++tap)
+                bad |= !all_finite4(acc[f][tap][0], acc[f][tap][1], acc[f][tap][2], acc[f][tap][3]);
+        if (bad) smem[a.flag] = 1.f;
+    }
 #pragma unroll
     for (int f = 0; f < WKF; ++f)
 #pragma unroll
@@ -1007,68 +1069,33 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
     __syncthreads();
     float *ob = a.out + (int64_t)split * a.split_stride;
     const int len = min(CT, a.C - c0) * RS;  // valid floats of a row
-    // A non-finite partial may hold a product the reference skips (a G value
-    // times the halo's padding, or a masked lane's zero times real x): it is
-    // recomputed over the block's output pixels, which are one contiguous
-    // range of the batch (exact.hpp).  As in the forward's epilogue, the
-    // first pass holds such values back and a second pass stores them.
-    auto fix = [&](int k, int e) __attribute__((always_inline)) {
+    if (smem[a.flag] != 0.f) {
+        // The block's output pixels are one contiguous range of the batch.
         const TileGeo g0 = geo(tb), g1 = geo(te - 1);
         const int64_t pbeg = ((int64_t)g0.n * a.OH + g0.oy0) * a.OW + g0.cx0;
         const int64_t pend = ((int64_t)g1.n * a.OH + g1.oy0 + g1.tr - 1) * a.OW + g1.cx1;
-        const int ce = e / RS, tap = e - (e / RS) * RS;
-        return exact_dw(a.x, a.g, a.C, a.H, a.W, a.K, a.OH, a.OW, a.st, a.pad, k, c0 + ce,
-                        tap / S, tap % S, pbeg, pend);
-    };
-    auto put = [&](float *dst, float v) __attribute__((always_inline)) {
-        if (a.split_stride == 0)
-            store_beta(dst, v, a.beta);
-        else
-            *dst = v;
-    };
-    bool held = false;
-    const bool vec = a.out_vec && len == CT * RS;
+        direct_dw_epilogue_exact<KT, RS, S>(a, ps, Geo::PPITCH, ob, k0, c0, len, pbeg, pend,
+                                            wave, lane);
+        return;
+    }
     for (int row = wave; row < KT; row += 4) {
         const int k = k0 + row;
         if (k >= a.K) break;
         float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
         const float *src = ps + row * Geo::PPITCH;
-        if (vec) {
+        if (a.out_vec && len == CT * RS) {
             for (int c4 = lane; c4 < CT * RS / 4; c4 += 64) {
                 floatx4 v = *reinterpret_cast<const floatx4 *>(src + c4 * 4);
-                if (!all_finite4(v[0], v[1], v[2], v[3])) {
-                    held = true;
-                    continue;
-                }
                 floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
                 if (a.split_stride == 0 && a.beta != 0.f) v += *d;
                 *d = v;
             }
         } else {
             for (int e = lane; e < len; e += 64) {
-                if (__builtin_isfinite(src[e]))
-                    put(dst + e, src[e]);
+                if (a.split_stride == 0)
+                    store_beta(dst + e, src[e], a.beta);
                 else
-                    held = true;
-            }
-        }
-    }
-    if (held) {
-        for (int row = wave; row < KT; row += 4) {
-            const int k = k0 + row;
-            if (k >= a.K) break;
-            float *dst = ob + (int64_t)k * a.CRS + c0 * RS;
-            const float *src = ps + row * Geo::PPITCH;
-            for (int e = vec ? lane * 4 : lane; e < len; e += vec ? 256 : 64) {
-                // A held-back 16-byte run is written element by element.
-                const int ne = vec ? 4 : 1;
-                bool any = false;
-                for (int q = 0; q < ne; ++q) any |= !__builtin_isfinite(src[e + q]);
-                if (!any) continue;
-                for (int q = 0; q < ne; ++q) {
-                    const float v = src[e + q];
-                    put(dst + e + q, __builtin_isfinite(v) ? v : fix(k, e + q));
-                }
+                    dst[e] = src[e];
             }
         }
     }

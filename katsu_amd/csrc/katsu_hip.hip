@@ -920,7 +920,9 @@ bool direct_dw_plan(const ConvDims &d, int64_t target_blocks, DirectDwPlan *pl) 
     const int64_t gcap = (trows * seg_w + 3) / 4 * 4;
     const int64_t gpitch = gcap % 4 == 0 ? gcap + 2 : gcap;  // == 2 (mod 4)
     const int64_t stage = KT * gpitch + Geo::XS;
-    const int64_t lds = std::max<int64_t>(2 * stage, (int64_t)KT * Geo::PPITCH) * 4;
+    // The stages (or the epilogue's transpose), then the block's flag word.
+    const int64_t flag = std::max<int64_t>(2 * stage, (int64_t)KT * Geo::PPITCH);
+    const int64_t lds = (flag + 4) * 4;
     if (lds > kLdsMax) return false;
     const int64_t segs = cdiv(d.OW, seg_w);
     const int64_t tiles_img = cdiv(d.OH, trows) * segs;
@@ -968,6 +970,7 @@ bool direct_dw_plan(const ConvDims &d, int64_t target_blocks, DirectDwPlan *pl) 
     a.beta = 0.f;
     a.fd_tiles_img = fdiv(tiles_img);
     a.fd_segs = fdiv(segs);
+    a.flag = (int)flag;
     pl->ok = true;
     pl->blocks = blocks;
     pl->splits = (int)splits;
