@@ -248,6 +248,18 @@ int katsu_hip_broadcast_rows_f32_dev(const float *g, size_t rows, size_t cols, f
 int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, size_t c,
                               size_t hw, float *cam, void *stream);
 
+/* Grad-CAM's last step, resizing each map to the original image
+ * (docs/conv2d.md, "O que falta para Grad-CAM": "redimensionar para a imagem
+ * original"): n maps [ih][iw] -> dst [n][oh][ow], bilinear with half-pixel
+ * centres.  Output row oy samples source row
+ * sy = max(0, (oy + 0.5) * ih/oh - 0.5) and blends rows floor(sy) and
+ * floor(sy) + 1 (clamped to ih - 1) with weights 1 - f and f,
+ * f = sy - floor(sy); columns likewise.  Equal sizes copy exactly.
+ * ih*iw and oh*ow must each be <= 2^31 - 1.  No counterpart in the
+ * reference's code. */
+int katsu_hip_resize_bilinear_f32_dev(const float *src, size_t n, size_t ih, size_t iw,
+                                      size_t oh, size_t ow, float *dst, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,7 @@ EXPORTS = (
     "katsu_hip_add_f32_dev", "katsu_hip_mul_f32_dev", "katsu_hip_accumulate_f32_dev",
     "katsu_hip_fill_f32_dev", "katsu_hip_add_scalar_f32_dev", "katsu_hip_sum_f32_dev",
     "katsu_hip_mean_rows_f32_dev", "katsu_hip_broadcast_rows_f32_dev",
-    "katsu_hip_gradcam_f32_dev",
+    "katsu_hip_gradcam_f32_dev", "katsu_hip_resize_bilinear_f32_dev",
 )
 
 
@@ -94,6 +94,7 @@ def lib():
         L.katsu_hip_mean_rows_f32_dev.argtypes = [vp, sz, sz, vp, vp]
         L.katsu_hip_broadcast_rows_f32_dev.argtypes = [vp, sz, sz, fp, vp, fp, vp]
         L.katsu_hip_gradcam_f32_dev.argtypes = [vp, vp, sz, sz, sz, vp, vp]
+        L.katsu_hip_resize_bilinear_f32_dev.argtypes = [vp, sz, sz, sz, sz, sz, vp, vp]
         for name in EXPORTS:
             if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown",
                             "katsu_hip_noalloc_scratch_bytes"):

@@ -731,19 +731,28 @@ std::optional<Tensor> Conv2D::get_activation_map() const {
 void Conv2D::clear_cache() const { last_forward_->reset(); }
 
 // Grad-CAM over get_activation_map() and its gradient, on the device.
-Result<Tensor> Conv2D::grad_cam() const {
+// With to_input_size, the maps are then resized to the input image
+// ("redimensionar para a imagem original", docs/conv2d.md).
+Result<Tensor> Conv2D::grad_cam(bool to_input_size) const {
     if (!*last_forward_) return err(TensorError::Kind::MissingForward);
-    const Tensor &map = (*last_forward_)->second;
+    const auto &[input, map] = **last_forward_;
     const TensorNode &n = *map.node_;
     if (!n.grad) return err(TensorError::Kind::MissingGradient);
     const auto &s = map.shape();
     KATSU_TRY(act, map.device_data());
     KATSU_TRY(count, element_count({s[0], s[2], s[3]}));
     KATSU_TRY(out, device_buffer(count));
-    const int rc = katsu_hip_gradcam_f32_dev(act, n.grad->get(), s[0], s[1], s[2] * s[3],
-                                             out.get(), stream());
+    int rc = katsu_hip_gradcam_f32_dev(act, n.grad->get(), s[0], s[1], s[2] * s[3], out.get(),
+                                       stream());
     if (rc != KATSU_OK) return device(rc);
-    return device_node(std::move(out), {s[0], s[2], s[3]}, Op{}, {}, count);
+    if (!to_input_size) return device_node(std::move(out), {s[0], s[2], s[3]}, Op{}, {}, count);
+    const auto &is = input.shape();
+    KATSU_TRY(rcount, element_count({is[0], is[2], is[3]}));
+    KATSU_TRY(resized, device_buffer(rcount));
+    rc = katsu_hip_resize_bilinear_f32_dev(out.get(), s[0], s[2], s[3], is[2], is[3],
+                                           resized.get(), stream());
+    if (rc != KATSU_OK) return device(rc);
+    return device_node(std::move(resized), {is[0], is[2], is[3]}, Op{}, {}, rcount);
 }
 
 }  // namespace katsu

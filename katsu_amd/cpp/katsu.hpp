@@ -201,11 +201,12 @@ class Conv2D {
     std::optional<Tensor> get_activation_map() const;
     void clear_cache() const;
     // Grad-CAM of the last forward's activation map, after a backward has
-    // given it a gradient: [N, OH, OW] maps (the method docs/conv2d.md
-    // outlines; the reference provides only the raw map): channel weights =
-    // spatial means of the gradient, ReLU of the weighted channel sum, each
-    // map divided by its maximum.  The maps are not resized to the input.
-    Result<Tensor> grad_cam() const;
+    // given it a gradient (the method docs/conv2d.md outlines; the reference
+    // provides only the raw map): channel weights = spatial means of the
+    // gradient, ReLU of the weighted channel sum, each map divided by its
+    // maximum: [N, OH, OW] maps; with to_input_size, each map resized
+    // bilinearly to the input image, [N, H, W].
+    Result<Tensor> grad_cam(bool to_input_size = false) const;
 
    private:
     Conv2D(Tensor w, size_t stride, size_t padding)

@@ -2512,4 +2512,17 @@ int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, siz
     return launch_status();
 }
 
+int katsu_hip_resize_bilinear_f32_dev(const float *src, size_t n, size_t ih, size_t iw,
+                                      size_t oh, size_t ow, float *dst, void *stream) {
+    if (n == 0 || oh == 0 || ow == 0) return KATSU_OK;
+    if (!src || !dst || ih == 0 || iw == 0) return KATSU_E_INVALID;
+    // Per-image offsets and pixel indices are 32-bit.
+    if (ih > kI32Max / iw || oh > kI32Max / ow || n > (size_t)kI32Max)
+        return KATSU_E_INVALID;
+    const int64_t total = (int64_t)n * (int64_t)(oh * ow);
+    resize_bilinear<<<ew_blocks(total), 256, 0, (hipStream_t)stream>>>(
+        src, (int64_t)n, (int)ih, (int)iw, (int)oh, (int)ow, dst);
+    return launch_status();
+}
+
 }  // extern "C"

@@ -208,10 +208,11 @@ def broadcast_rows(g, rows, cols, scale, dy=None, beta=0.0):
     return dy
 
 
-def grad_cam(act, grad):
+def grad_cam(act, grad, size=None):
     """Grad-CAM of an NCHW activation map and its gradient: [N, H, W] maps,
     ReLU of the channel sum weighted by the gradient's spatial means, each
-    divided by its maximum."""
+    divided by its maximum; with size=(OH, OW), each map then resized to the
+    original image by resize_bilinear."""
     _dev_f32(act, grad)
     if act.shape != grad.shape or act.dim() != 4:
         raise ValueError("activation and gradient must be the same NCHW shape")
@@ -219,4 +220,17 @@ def grad_cam(act, grad):
     cam = torch.empty((n, h, w), device=act.device, dtype=torch.float32)
     check(lib().katsu_hip_gradcam_f32_dev(_p(act), _p(grad), n, c, h * w, _p(cam), _stream()),
           "grad_cam")
-    return cam
+    return cam if size is None else resize_bilinear(cam, size)
+
+
+def resize_bilinear(maps, size):
+    """[N, H, W] maps resized to [N, OH, OW]: bilinear, half-pixel centres."""
+    _dev_f32(maps)
+    if maps.dim() != 3:
+        raise ValueError("maps must be [N, H, W]")
+    n, h, w = maps.shape
+    oh, ow = (int(v) for v in size)
+    out = torch.empty((n, oh, ow), device=maps.device, dtype=torch.float32)
+    check(lib().katsu_hip_resize_bilinear_f32_dev(_p(maps), n, h, w, oh, ow, _p(out),
+                                                   _stream()), "resize_bilinear")
+    return out

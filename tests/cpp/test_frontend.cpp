@@ -429,6 +429,41 @@ void grad_cam_on_device() {
     }
 }
 
+// Grad-CAM resized to the input image on a stride-2 layer ([2,3,12,10] ->
+// maps [2,6,5] -> [2,12,10]): the resized maps equal the bilinear
+// half-pixel-centre formula, evaluated in double on the host from the
+// unresized maps; the unresized call is unchanged by the option.
+void grad_cam_resized_to_input() {
+    auto layer = TRY(Conv2D::new_seeded(3, 8, {3, 3}, 2, 1, 321));
+    V xs(2 * 3 * 12 * 10);
+    for (size_t i = 0; i < xs.size(); ++i) xs[i] = (float)((i * 37) % 251) / 125.0f - 1.0f;
+    auto x = TRY(Tensor::create(xs, {2, 3, 12, 10}));
+    auto y = TRY(layer.forward(x));
+    CHECK(y.shape() == (std::vector<size_t>{2, 8, 6, 5}));
+    TRY(TRY(TRY(y.mul(y)).sum()).backward());
+    auto small = TRY(layer.grad_cam());
+    auto big = TRY(layer.grad_cam(true));
+    CHECK(small.shape() == (std::vector<size_t>{2, 6, 5}));
+    CHECK(big.shape() == (std::vector<size_t>{2, 12, 10}));
+    const V &s = small.data(), &b = big.data();
+    const size_t IH = 6, IW = 5, OH = 12, OW = 10;
+    double worst = 0;
+    for (size_t n = 0; n < 2; ++n)
+        for (size_t oy = 0; oy < OH; ++oy)
+            for (size_t ox = 0; ox < OW; ++ox) {
+                const double sy = std::fmax((oy + 0.5) * IH / OH - 0.5, 0.0);
+                const double sx = std::fmax((ox + 0.5) * IW / OW - 0.5, 0.0);
+                const size_t y0 = std::min((size_t)sy, IH - 1), x0 = std::min((size_t)sx, IW - 1);
+                const size_t y1 = std::min(y0 + 1, IH - 1), x1 = std::min(x0 + 1, IW - 1);
+                const double fy = sy - y0, fx = sx - x0;
+                const float *m = s.data() + n * IH * IW;
+                const double want = (1 - fy) * ((1 - fx) * m[y0 * IW + x0] + fx * m[y0 * IW + x1]) +
+                                    fy * ((1 - fx) * m[y1 * IW + x0] + fx * m[y1 * IW + x1]);
+                worst = std::fmax(worst, std::fabs(b[(n * OH + oy) * OW + ox] - want));
+            }
+    CHECK(worst <= 1e-6);
+}
+
 // backward_with publishes all gradients or none (tensor.rs:341-360): a device
 // failure after the first node's accumulation leaves every stored gradient
 // as it was; the next pass accumulates into all of them.
@@ -489,6 +524,7 @@ const Case kCases[] = {
     {"known_stride_and_padding", known_stride_and_padding},
     {"stem_chain_on_device", stem_chain_on_device},
     {"grad_cam_on_device", grad_cam_on_device},
+    {"grad_cam_resized_to_input", grad_cam_resized_to_input},
     {"publish_is_all_or_nothing", publish_is_all_or_nothing},
 };
 

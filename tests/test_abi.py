@@ -101,6 +101,20 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert L.katsu_hip_conv2d_fwd_f32(p, p, p, ctypes.byref(g)) == _abi.E_INVALID
 
 
+def test_resize_bilinear_rejects_before_any_launch():
+    """Grad-CAM's resize: null buffers and per-image sizes past the 32-bit
+    index range are refused; empty outputs need no device."""
+    L = katsu_amd.lib()
+    buf = (ctypes.c_float * 4)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert L.katsu_hip_resize_bilinear_f32_dev(None, 1, 4, 4, 8, 8, p, None) == _abi.E_INVALID
+    assert L.katsu_hip_resize_bilinear_f32_dev(p, 1, 0, 4, 8, 8, p, None) == _abi.E_INVALID
+    assert L.katsu_hip_resize_bilinear_f32_dev(p, 1, 4, 4, 1 << 16, 1 << 16, p,
+                                               None) == _abi.E_INVALID
+    assert L.katsu_hip_resize_bilinear_f32_dev(None, 0, 4, 4, 8, 8, None, None) == _abi.OK
+    assert L.katsu_hip_resize_bilinear_f32_dev(None, 2, 4, 4, 0, 8, None, None) == _abi.OK
+
+
 def test_empty_problems_need_no_device():
     """tests/tensor.rs:65-86 at the ABI: [2,0]@[0,3] gives six zeros (beta 0) or
     leaves C alone (beta 1); N = 0 leaves dW = beta*dW (tests/conv2d.rs:156-167).

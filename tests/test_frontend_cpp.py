@@ -43,6 +43,7 @@ DEVICE = [
 EXTRA_DEVICE = [
     "stem_chain_on_device",
     "grad_cam_on_device",
+    "grad_cam_resized_to_input",
     "publish_is_all_or_nothing",
 ]
 

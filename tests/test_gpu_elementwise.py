@@ -115,3 +115,51 @@ def test_grad_cam(dev):
     ref = np.where(mx[:, None, None] > 0, ref / np.where(mx > 0, mx, 1)[:, None, None], 0.0)
     assert np.all(cam[2] == 0.0)
     assert np.max(np.abs(cam - ref)) <= 1e-5
+
+
+@pytest.mark.parametrize("src,dst", [((14, 15), (28, 30)), ((112, 112), (224, 224)),
+                                     ((14, 15), (7, 4)), ((6, 5), (6, 5)), ((1, 3), (5, 9))])
+def test_resize_bilinear(dev, src, dst):
+    """katsu_hip_resize_bilinear_f32_dev (Grad-CAM's resize to the input image)
+    against torch's CPU bilinear interpolation in float64 with half-pixel
+    centres (align_corners=False), an independent implementation of the same
+    formula; equal sizes copy bit for bit."""
+    import torch
+    import torch.nn.functional as F
+
+    from katsu_amd import ops
+    n = 3
+    maps = np.abs(synth.uniform(21, (n, *src)))
+    got = ops.resize_bilinear(torch.from_numpy(maps).to(dev), dst).cpu().numpy()
+    ref = F.interpolate(torch.from_numpy(maps.astype(np.float64))[:, None], size=dst,
+                        mode="bilinear", align_corners=False)[:, 0].numpy()
+    assert got.shape == (n, *dst)
+    assert np.max(np.abs(got - ref)) <= 2e-7
+    if src == dst:
+        assert np.array_equal(got, maps)
+
+
+def test_grad_cam_resized(dev):
+    """Grad-CAM with the resize: the unresized maps, then resized, equal the
+    maps computed with size= in one call; and the resized maps are within
+    1e-5 of the float64 formula followed by torch's float64 bilinear resize."""
+    import torch
+    import torch.nn.functional as F
+
+    from katsu_amd import ops
+    n, c, h, w = 2, 8, 7, 9
+    act = synth.uniform(31, (n, c, h, w))
+    grad = synth.uniform(32, (n, c, h, w))
+    a, g = torch.from_numpy(act).to(dev), torch.from_numpy(grad).to(dev)
+    small = ops.grad_cam(a, g)
+    big = ops.grad_cam(a, g, size=(14, 18)).cpu().numpy()
+    assert np.array_equal(big, ops.resize_bilinear(small, (14, 18)).cpu().numpy())
+    a64, g64 = act.astype(np.float64), grad.astype(np.float64)
+    alpha = g64.reshape(n, c, -1).mean(2)
+    ref = np.maximum(np.einsum("nc,nchw->nhw", alpha, a64), 0.0)
+    mx = ref.reshape(n, -1).max(1)
+    ref = np.where(mx[:, None, None] > 0, ref / np.where(mx > 0, mx, 1)[:, None, None], 0.0)
+    ref = F.interpolate(torch.from_numpy(ref)[:, None], size=(14, 18), mode="bilinear",
+                        align_corners=False)[:, 0].numpy()
+    assert np.max(np.abs(big - ref)) <= 1e-5
+
