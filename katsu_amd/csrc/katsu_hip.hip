@@ -1378,12 +1378,45 @@ int64_t tiny_dx_lds(const ConvDims &d) {
     return ((int64_t)d.K * d.RS * 4 + (int64_t)d.K * d.R * d.OW) * 4;
 }
 
-bool tiny_ok(const ConvDims &d) {
+// The row kernels (tiny_*_kernel): any filter up to 32 x 8, any stride.
+bool tiny_rows_ok(const ConvDims &d) {
     return d.C <= kTinyC && d.K <= kTinyK && (int64_t)d.K * d.CRS <= kTinyW && d.S <= 8 &&
            d.R <= 32 && (int64_t)d.CHW * 4 < (int64_t)kMaxBufBytes &&
            (int64_t)d.KOHW * 4 < (int64_t)kMaxBufBytes &&
            tiny_fwd_lds(d) <= 65536 && tiny_dx_lds(d) <= 65536 &&
            (int64_t)d.N * std::max(d.OH, d.H) <= kI32Max;
+}
+bool tiny3_ok(const ConvDims &d);
+// Few-channel layers: the register forms where they apply, else the row kernels.
+bool tiny_ok(const ConvDims &d) { return tiny3_ok(d) || tiny_rows_ok(d); }
+
+// The register forms (tiny3_*): 3x3 filters, stride 1 or 2, output rows of at
+// least 4 pixels (the dW walk wraps a row at most once per step).  Their
+// grids are (images x pixel parts [x channels]), kept in 32 bits.
+#ifndef KATSU_TINY3_KG
+#define KATSU_TINY3_KG 4  // forward outputs per thread
+#endif
+#ifndef KATSU_TINY3_STEPS
+#define KATSU_TINY3_STEPS 16  // dW MFMA k-steps (4 pixels each) per wave and tile
+#endif
+#ifndef KATSU_TINY3_DW_BLOCKS
+#define KATSU_TINY3_DW_BLOCKS 512  // at most this many dW partials
+#endif
+constexpr size_t kTiny3DwLds = 4 * 3 * 64 * 4 * sizeof(float);  // 4 waves x NF <= 3 tiles
+int tiny3_nf(const ConvDims &d) { return (int)cdiv((int64_t)d.C * 9, 16); }
+bool tiny3_ok(const ConvDims &d) {
+    return d.C <= kTinyC && d.K <= kTinyK && d.R == 3 && d.S == 3 && (d.st == 1 || d.st == 2) &&
+           d.OW >= 4 &&
+           (int64_t)d.CHW * 4 < (int64_t)kMaxBufBytes &&
+           (int64_t)d.KOHW * 4 < (int64_t)kMaxBufBytes &&
+           (int64_t)d.N * cdiv((int64_t)d.H * d.W, 256) * d.C <= kI32Max &&
+           (int64_t)d.N * cdiv((int64_t)d.OH * d.OW, 256) <= kI32Max;
+}
+int64_t tiny3_dw_pb(const ConvDims &d) {
+    return cdiv((int64_t)d.OH * d.OW, 16 * KATSU_TINY3_STEPS);
+}
+int64_t tiny3_dw_blocks(const ConvDims &d) {
+    return std::min<int64_t>((int64_t)d.N * tiny3_dw_pb(d), KATSU_TINY3_DW_BLOCKS);
 }
 
 TinyArgs tiny_args(const ConvDims &d) {
@@ -1402,11 +1435,25 @@ TinyArgs tiny_args(const ConvDims &d) {
     return a;
 }
 
+template <int KG>
+int tiny3_fwd_launch(const TinyArgs &a, const float *w, const ConvDims &d, hipStream_t st) {
+    const int64_t pb = cdiv((int64_t)d.OH * d.OW, 256);
+    tiny3_fwd_kernel<KG><<<dim3((unsigned)(d.N * pb), (unsigned)cdiv(d.K, KG)), dim3(256), 0,
+                           st>>>(a, w, (int)pb);
+    return launch_status();
+}
+
 int tiny_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
     TinyArgs a = tiny_args(d);
     a.x = x;
     a.w = w;
     a.out = y;
+    if (tiny3_ok(d)) {
+        const int kg = std::min(KATSU_TINY3_KG, d.K);
+        return kg >= 4 ? tiny3_fwd_launch<4>(a, w, d, st)
+               : kg >= 2 ? tiny3_fwd_launch<2>(a, w, d, st)
+                         : tiny3_fwd_launch<1>(a, w, d, st);
+    }
     a.xw = (int)tiny_xw(d);
     const dim3 grid((unsigned)((int64_t)d.N * d.OH));
     const size_t lds = (size_t)tiny_fwd_lds(d);
@@ -1418,6 +1465,20 @@ int tiny_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStr
     return launch_status();
 }
 
+// dX register form: KB output channels summed per thread (the K bucket),
+// stride 1 or 2; ndx blocks of pixel parts pb, or 0 when it does not apply.
+template <int ST>
+int tiny3_dx_launch_st(const TinyArgs &a, const float *w, const ConvDims &d, hipStream_t st) {
+    const int64_t pb = cdiv((int64_t)d.H * d.W, 256);
+    const dim3 grid((unsigned)(d.C * d.N * pb));
+    switch (tiny_kb(d)) {
+        case 4: tiny3_dx_kernel<4, ST><<<grid, dim3(256), 0, st>>>(a, w, (int)pb); break;
+        case 8: tiny3_dx_kernel<8, ST><<<grid, dim3(256), 0, st>>>(a, w, (int)pb); break;
+        default: tiny3_dx_kernel<16, ST><<<grid, dim3(256), 0, st>>>(a, w, (int)pb); break;
+    }
+    return launch_status();
+}
+
 int tiny_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float beta,
             hipStream_t st) {
     TinyArgs a = tiny_args(d);
@@ -1425,9 +1486,45 @@ int tiny_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float
     a.w = w;
     a.out = dx;
     a.beta = beta;
+    if (tiny3_ok(d))
+        return d.st == 1 ? tiny3_dx_launch_st<1>(a, w, d, st) : tiny3_dx_launch_st<2>(a, w, d, st);
     tiny_dx_kernel<<<dim3((unsigned)((int64_t)d.N * d.H)), dim3(256), (size_t)tiny_dx_lds(d),
                      st>>>(a, w);
     return launch_status();
+}
+
+// Both register-form passes in one launch: the dX blocks (channel x image x
+// pixel part), then the dW partial blocks.
+template <int KB, int ST, int NF>
+int tiny3_bwd_launch_t(const TinyArgs &a, const float *w, const ConvDims &d, int64_t dwblocks,
+                       size_t lds, hipStream_t st) {
+    const int64_t pbx = cdiv((int64_t)d.H * d.W, 256);
+    const int64_t ndx = (int64_t)d.C * d.N * pbx;
+    if (ndx + dwblocks > kI32Max) return KATSU_E_INVALID;
+    tiny3_bwd_kernel<KB, ST, NF, KATSU_TINY3_STEPS>
+        <<<dim3((unsigned)(ndx + dwblocks)), dim3(256), lds, st>>>(a, w, (int)ndx, (int)pbx,
+                                                                  (int)tiny3_dw_pb(d));
+    return launch_status();
+}
+
+template <int KB, int ST>
+int tiny3_bwd_launch_kb(const TinyArgs &a, const float *w, const ConvDims &d, int64_t dwblocks,
+                        size_t lds, hipStream_t st) {
+    switch (tiny3_nf(d)) {
+        case 1: return tiny3_bwd_launch_t<KB, ST, 1>(a, w, d, dwblocks, lds, st);
+        case 2: return tiny3_bwd_launch_t<KB, ST, 2>(a, w, d, dwblocks, lds, st);
+        default: return tiny3_bwd_launch_t<KB, ST, 3>(a, w, d, dwblocks, lds, st);
+    }
+}
+
+template <int ST>
+int tiny3_bwd_launch_st(const TinyArgs &a, const float *w, const ConvDims &d, int64_t dwblocks,
+                        size_t lds, hipStream_t st) {
+    switch (tiny_kb(d)) {
+        case 4: return tiny3_bwd_launch_kb<4, ST>(a, w, d, dwblocks, lds, st);
+        case 8: return tiny3_bwd_launch_kb<8, ST>(a, w, d, dwblocks, lds, st);
+        default: return tiny3_bwd_launch_kb<16, ST>(a, w, d, dwblocks, lds, st);
+    }
 }
 
 // dW: one partial per block of output rows, about one block per CU.
@@ -1443,10 +1540,18 @@ TinyDwPlan tiny_dw_plan(const ConvDims &d) {
     const int64_t rows = (int64_t)d.N * d.OH;
     const int64_t xw = (int64_t)(d.OW - 1) * d.st + d.S;
     const int64_t lds = ((int64_t)d.K * d.OW + (int64_t)d.C * d.R * xw) * 4;
-    if (rows <= 0 || lds > 65536) return pl;
+    pl.pstride = ((int64_t)d.K * d.CRS + 3) / 4 * 4;
+    if (rows <= 0) return pl;
+    if (tiny3_ok(d)) {
+        pl.blocks = tiny3_dw_blocks(d);
+        pl.lds = kTiny3DwLds;
+        pl.ws_bytes = (size_t)pl.blocks * (size_t)pl.pstride * sizeof(float);
+        pl.ok = true;
+        return pl;
+    }
+    if (lds > 65536) return pl;
     pl.rows_per_block = cdiv(rows, kMinDirectBlocks);
     pl.blocks = cdiv(rows, pl.rows_per_block);
-    pl.pstride = ((int64_t)d.K * d.CRS + 3) / 4 * 4;
     pl.xw = xw;
     pl.lds = (size_t)lds;
     pl.ws_bytes = (size_t)pl.blocks * (size_t)pl.pstride * sizeof(float);
@@ -1463,11 +1568,33 @@ int tiny_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const
     a.rows_per_block = (int)pl.rows_per_block;
     a.xw = (int)pl.xw;
     a.pstride = pl.pstride;
-    tiny_dw_kernel<<<dim3((unsigned)pl.blocks), dim3(256), pl.lds, st>>>(a);
+    if (tiny3_ok(d)) {
+        const int pb = (int)tiny3_dw_pb(d);
+        const dim3 grid((unsigned)pl.blocks);
+        switch (tiny3_nf(d)) {
+            case 1:
+                tiny3_dw_kernel<1, KATSU_TINY3_STEPS><<<grid, dim3(256), pl.lds, st>>>(a, pb);
+                break;
+            case 2:
+                tiny3_dw_kernel<2, KATSU_TINY3_STEPS><<<grid, dim3(256), pl.lds, st>>>(a, pb);
+                break;
+            default:
+                tiny3_dw_kernel<3, KATSU_TINY3_STEPS><<<grid, dim3(256), pl.lds, st>>>(a, pb);
+                break;
+        }
+    } else {
+        tiny_dw_kernel<<<dim3((unsigned)pl.blocks), dim3(256), pl.lds, st>>>(a);
+    }
     const int rc = launch_status();
     if (rc != KATSU_OK) return rc;
     return launch_split_reduce(ws, dw, (int64_t)d.K * d.CRS, pl.pstride, (int)pl.blocks, beta,
                                st);
+}
+
+int tiny3_bwd_launch(const TinyArgs &a, const float *w, const ConvDims &d, const TinyDwPlan &pl,
+                     hipStream_t st) {
+    return d.st == 1 ? tiny3_bwd_launch_st<1>(a, w, d, pl.blocks, pl.lds, st)
+                     : tiny3_bwd_launch_st<2>(a, w, d, pl.blocks, pl.lds, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -1912,11 +2039,16 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
             a.rows_per_block = (int)tp.rows_per_block;
             a.xw = (int)tp.xw;
             a.pstride = tp.pstride;
-            const int64_t ndx = (int64_t)d.N * d.H;
-            const size_t lds = std::max((size_t)tiny_dx_lds(d), tp.lds);
-            tiny_bwd_kernel<<<dim3((unsigned)(ndx + tp.blocks)), dim3(256), lds, st>>>(a, w,
-                                                                                      (int)ndx);
-            if ((rc = launch_status()) != KATSU_OK) return rc;
+            if (tiny3_ok(d))
+                rc = tiny3_bwd_launch(a, w, d, tp, st);
+            else {
+                const int64_t ndx = (int64_t)d.N * d.H;
+                const size_t lds = std::max((size_t)tiny_dx_lds(d), tp.lds);
+                tiny_bwd_kernel<<<dim3((unsigned)(ndx + tp.blocks)), dim3(256), lds, st>>>(
+                    a, w, (int)ndx);
+                rc = launch_status();
+            }
+            if (rc != KATSU_OK) return rc;
             return launch_split_reduce(wsp, dw, (int64_t)d.K * d.CRS, tp.pstride, (int)tp.blocks,
                                        beta, st);
         }

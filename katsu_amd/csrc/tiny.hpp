@@ -289,4 +289,343 @@ __global__ void __launch_bounds__(256)
         tiny_dw_block(a, sm, blockIdx.x - ndx);
 }
 
+// ---------------------------------------------------------------------------
+// Register forms for 3x3 filters (config 1's layer).  The row kernels above
+// put one block on each image row, which leaves most SIMDs with one wave
+// and serialises each block's staging, barrier and compute.  These instead
+// give every thread one output element group and no barrier: each thread
+// issues all of its loads at once (buffer loads; a padded or absent tap gets
+// an out-of-range offset and reads zero without a branch), then sums.  The
+// weights are uniform across the block and read as such.  The sums keep the
+// orders above, and a padded tap is skipped by a select (acc unchanged), as
+// the reference skips it, so the forward and dX equal the reference bit for
+// bit whatever the data, NaN and Inf included.
+
+// Forward: thread = (output pixel p of image n, outputs k0 .. k0+KG-1).
+// Block b covers pixels [256*(b % pb), +256) of image b / pb; blockIdx.y
+// is the output group.  The block's weights go to LDS as [c][r][s][KG]
+// (zeros past C and K) while the input loads are in flight.  With finite
+// weights a padded tap's zero input adds an exact +-0 to a sum that is never
+// -0 (it starts at +0, and round-to-nearest never turns a sum of other
+// values into -0), so it leaves the sum as skipping it would; a non-finite
+// weight makes the block skip padded taps explicitly.
+template <int KG>
+__global__ void __launch_bounds__(256)
+    tiny3_fwd_kernel(const TinyArgs a, const float *__restrict__ w, int pb) {
+#pragma clang fp contract(off)
+    constexpr int R = 3, S = 3, CC = kTinyC, NW = CC * R * S * KG;
+    static_assert(NW <= 256, "one weight per thread");
+    __shared__ float wt[NW];
+    __shared__ int nonfinite;
+    const int t = threadIdx.x;
+    if (t == 0) nonfinite = 0;
+    const int n = blockIdx.x / pb, pblk = blockIdx.x - n * pb;
+    const int k0 = blockIdx.y * KG;
+    const int crs = a.C * R * S;
+    // Thread t < NW fetches weight (tap t / KG, output k0 + t % KG), tap =
+    // (c*R + r)*S + s; the load is issued first and used after the input
+    // loads, so the two round trips overlap.
+    const int wq = t % KG, wtap = t / KG;
+    const bool wok = t < NW && wtap < crs && k0 + wq < a.K;
+    float wraw = w[wok ? (k0 + wq) * crs + wtap : 0];
+    const int ohw = a.OH * a.OW;
+    const int p0 = pblk * 256 + t;
+    const bool live = p0 < ohw;
+    const int p = live ? p0 : ohw - 1;
+    const int oy = p / a.OW, ox = p - oy * a.OW;
+    const int iy0 = oy * a.st - a.pad, ix0 = ox * a.st - a.pad;
+    const int hw = a.H * a.W;
+    const int64_t chw = (int64_t)a.C * hw;
+    const auto rx = buf_rsrc(a.x + n * chw, (uint32_t)(chw * 4));
+    bool rok[R], cok[S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rok[r] = (unsigned)(iy0 + r) < (unsigned)a.H;
+#pragma unroll
+    for (int s = 0; s < S; ++s) cok[s] = (unsigned)(ix0 + s) < (unsigned)a.W;
+    const int base = iy0 * a.W + ix0;
+    float xv[CC][R][S];
+#pragma unroll
+    for (int c = 0; c < CC; ++c)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const bool v = c < a.C && rok[r] && cok[s];
+                xv[c][r][s] = buf_load(rx, v ? (c * hw + base + r * a.W + s) * 4 : kOOB);
+            }
+    // An unconditional use here keeps the weight load ahead of the input
+    // loads (the compiler would otherwise sink it into the store below).
+    asm volatile("" : "+v"(wraw));
+    __syncthreads();  // nonfinite = 0 is visible before any thread sets it
+    if (t < NW) {
+        const float wv = wok ? wraw : 0.f;
+        wt[t] = wv;
+        if (!__builtin_isfinite(wv)) nonfinite = 1;
+    }
+    __syncthreads();
+    const bool skip = nonfinite != 0;
+    float acc[KG];
+#pragma unroll
+    for (int q = 0; q < KG; ++q) acc[q] = 0.f;
+    if (!skip) {
+#pragma unroll
+        for (int c = 0; c < CC; ++c) {
+            if (c >= a.C) continue;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float *wp = wt + ((c * R + r) * S + s) * KG;
+#pragma unroll
+                    for (int q = 0; q < KG; ++q) acc[q] = acc[q] + xv[c][r][s] * wp[q];
+                }
+        }
+    } else {
+        // A padded tap's product is replaced by +0, which leaves acc as it is.
+#pragma unroll
+        for (int c = 0; c < CC; ++c) {
+            if (c >= a.C) continue;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float *wp = wt + ((c * R + r) * S + s) * KG;
+                    const bool v = rok[r] && cok[s];
+#pragma unroll
+                    for (int q = 0; q < KG; ++q) {
+                        const float prod = xv[c][r][s] * wp[q];
+                        acc[q] = acc[q] + (v ? prod : 0.f);
+                    }
+                }
+        }
+    }
+    if (!live) return;
+    float *yp = a.out + ((int64_t)n * a.K + k0) * ohw + p;
+#pragma unroll
+    for (int q = 0; q < KG; ++q)
+        if (k0 + q < a.K) yp[(int64_t)q * ohw] = acc[q];
+}
+
+// dX: thread = (input pixel p of image n, channel c).  Block b covers
+// pixels [256*(b % pb), +256) of image (b / pb) % N, channel b / (pb*N).
+// Tap r reaches output row (iy + pad - r)/ST when that divides and lies
+// inside; the sum runs over k ascending, then r and s descending (the order
+// the reference's scatter adds into dx).  The block's weights w[k][c][.][.]
+// go to LDS as [k][r][s]; absent taps read G as zero, which (as in the
+// forward) leaves the sum unchanged unless a weight is non-finite, when the
+// block skips them explicitly.
+template <int KB, int ST>
+__device__ __forceinline__ void tiny3_dx_block(const TinyArgs &a, const float *__restrict__ w,
+                                               float *wt, int pb, int bid) {
+#pragma clang fp contract(off)
+    constexpr int R = 3, S = 3, NW = KB * R * S;
+    static_assert(NW <= 256, "one weight per thread");
+    int *nonfinite = reinterpret_cast<int *>(wt + NW);
+    const int t = threadIdx.x;
+    if (t == 0) *nonfinite = 0;
+    const int npb = a.N * pb;
+    const int c = bid / npb, rem = bid - c * npb;
+    const int n = rem / pb, pblk = rem - n * pb;
+    const int crs = a.C * R * S;
+    // Thread t < NW fetches w[k][c][r][s] for k = t / (R*S); the load is
+    // issued first and used after the G loads, so the round trips overlap.
+    const int wk = t / (R * S), wrs = t - wk * (R * S);
+    const bool wok = t < NW && wk < a.K;
+    float wraw = w[wok ? wk * crs + c * (R * S) + wrs : 0];
+    const int hw = a.H * a.W;
+    const int p0 = pblk * 256 + t;
+    const bool live = p0 < hw;
+    const int p = live ? p0 : hw - 1;
+    const int iy = p / a.W, ix = p - iy * a.W;
+    const int ohw = a.OH * a.OW;
+    bool rok[R], cok[S];
+    int oyo[R], oxo[S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int u = iy + a.pad - r;
+        rok[r] = u >= 0 && u % ST == 0 && u / ST < a.OH;
+        oyo[r] = (u / ST) * a.OW;
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int u = ix + a.pad - s;
+        cok[s] = u >= 0 && u % ST == 0 && u / ST < a.OW;
+        oxo[s] = u / ST;
+    }
+    const int64_t kohw = (int64_t)a.K * ohw;
+    const auto rg = buf_rsrc(a.g + n * kohw, (uint32_t)(kohw * 4));
+    float gv[KB][R][S];
+#pragma unroll
+    for (int k = 0; k < KB; ++k)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const bool v = k < a.K && rok[r] && cok[s];
+                gv[k][r][s] = buf_load(rg, v ? (k * ohw + oyo[r] + oxo[s]) * 4 : kOOB);
+            }
+    // An unconditional use here keeps the weight load ahead of the G loads
+    // (the compiler would otherwise sink it into the store below).
+    asm volatile("" : "+v"(wraw));
+    __syncthreads();  // *nonfinite = 0 is visible before any thread sets it
+    if (t < NW) {
+        const float wv = wok ? wraw : 0.f;
+        wt[t] = wv;
+        if (!__builtin_isfinite(wv)) *nonfinite = 1;
+    }
+    __syncthreads();
+    const bool skip = *nonfinite != 0;
+    float acc = 0.f;
+    if (!skip) {
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k >= a.K) continue;
+#pragma unroll
+            for (int r = R - 1; r >= 0; --r)
+#pragma unroll
+                for (int s = S - 1; s >= 0; --s)
+                    acc = acc + gv[k][r][s] * wt[(k * R + r) * S + s];
+        }
+    } else {
+        // An absent tap's product is replaced by +0, which leaves acc as it is.
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k >= a.K) continue;
+#pragma unroll
+            for (int r = R - 1; r >= 0; --r)
+#pragma unroll
+                for (int s = S - 1; s >= 0; --s) {
+                    const float prod = gv[k][r][s] * wt[(k * R + r) * S + s];
+                    acc = acc + (rok[r] && cok[s] ? prod : 0.f);
+                }
+        }
+    }
+    if (!live) return;
+    float *dp = a.out + ((int64_t)n * a.C + c) * hw + p;
+    *dp = a.beta == 0.f ? acc : *dp + acc;
+}
+
+template <int KB, int ST>
+__global__ void __launch_bounds__(256)
+    tiny3_dx_kernel(const TinyArgs a, const float *__restrict__ w, int pb) {
+    __shared__ float wt[KB * 9 + 1];  // weights, then the non-finite flag
+    tiny3_dx_block<KB, ST>(a, w, wt, pb, blockIdx.x);
+}
+
+// dW partials on the matrix cores: per block, dw[k][crs] = sum over its
+// output pixels of G[k][p] * X[crs][p] (crs = (c*3 + r)*3 + s, X the input
+// tap under pixel p), a 16 x (16*NF) tile fed 4 pixels per
+// v_mfma_f32_16x16x4_f32.  Block b of nb takes tiles b, b + nb, ... (tile
+// t: pixels [TP*(t % pb), +TP) of image t / pb, TP = 16*STEPS); wave v the
+// quarter [TP/4*v, +TP/4) of each, lane l (l/16 = pixel slot q, l%16 = i)
+// loading G[k = i] and the taps crs = 16f + i of pixels 4j + q, j < STEPS,
+// all in flight at once.  A padded or absent tap reads zero, which leaves a
+// finite sum as skipping it would; the four waves' tiles are added in wave
+// order through LDS, and a non-finite result is recomputed over the block's
+// pixels in the reference's order with padded taps skipped (exact_dw).  The
+// partial row goes to out2[b*pstride + k*crs_n + crs] for dw_split_reduce.
+template <int NF, int STEPS>
+__device__ __forceinline__ void tiny3_dw_block(const TinyArgs &a, float *sm, int pb, int nb,
+                                               int bid) {
+    constexpr int TP = 16 * STEPS;
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int ohw = a.OH * a.OW, hw = a.H * a.W;
+    const int64_t chw = (int64_t)a.C * hw, kohw = (int64_t)a.K * ohw;
+    const int crs_n = a.C * 9;
+    int toff[NF], tr[NF], ts[NF];
+    bool tval[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int crs = f * 16 + i;
+        tval[f] = crs < crs_n;
+        const int c = crs / 9, rs = crs - c * 9;
+        tr[f] = rs / 3;
+        ts[f] = rs - tr[f] * 3;
+        toff[f] = c * hw;
+    }
+    floatx4 acc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int ntiles = a.N * pb;
+    for (int t = bid; t < ntiles; t += nb) {
+        const int n = t / pb, part = t - n * pb;
+        const int pbeg = part * TP + wv * (TP / 4);
+        const int pend = min(part * TP + TP, ohw);
+        const auto rx = buf_rsrc(a.x + n * chw, (uint32_t)(chw * 4));
+        const auto rg = buf_rsrc(a.g + n * kohw, (uint32_t)(kohw * 4));
+        int p = pbeg + q;
+        int oy = p / a.OW, ox = p - (p / a.OW) * a.OW;
+        float av[STEPS], bv[STEPS][NF];
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            const bool pin = p < pend;
+            av[j] = buf_load(rg, pin && i < a.K ? (i * ohw + oy * a.OW + ox) * 4 : kOOB);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const int iy = oy * a.st - a.pad + tr[f], ix = ox * a.st - a.pad + ts[f];
+                const bool v = pin && tval[f] && (unsigned)iy < (unsigned)a.H &&
+                               (unsigned)ix < (unsigned)a.W;
+                bv[j][f] = buf_load(rx, v ? (toff[f] + iy * a.W + ix) * 4 : kOOB);
+            }
+            p += 4;
+            ox += 4;  // OW >= 4 (checked by the host): at most one wrap
+            if (ox >= a.OW) {
+                ox -= a.OW;
+                ++oy;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j][f], acc[f], 0, 0, 0);
+    }
+    // The four waves' tiles, added in wave order: element e = (f*64 + l)*4 + v
+    // of a tile is D[k = 4*(l/16) + v][crs = 16f + l%16].
+    floatx4 *red = reinterpret_cast<floatx4 *>(sm);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) red[(wv * NF + f) * 64 + lane] = acc[f];
+    __syncthreads();
+    const float *rs4 = sm;
+    for (int e = threadIdx.x; e < NF * 256; e += 256) {
+        const int f = e >> 8, l = (e >> 2) & 63, v = e & 3;
+        const int k = 4 * (l >> 4) + v, crs = 16 * f + (l & 15);
+        float sum = rs4[e];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) sum = sum + rs4[w * NF * 256 + e];
+        if (k >= a.K || crs >= crs_n) continue;
+        if (!__builtin_isfinite(sum)) {
+            const int c = crs / 9, r = (crs - c * 9) / 3, s2 = crs - c * 9 - r * 3;
+            sum = 0.f;
+            for (int t = bid; t < ntiles; t += nb) {
+                const int n = t / pb, part = t - n * pb;
+                const int64_t b0 = (int64_t)n * ohw + (int64_t)part * TP;
+                const int64_t b1 = (int64_t)n * ohw + min(part * TP + TP, ohw);
+                sum = sum + exact_dw(a.x, a.g, a.C, a.H, a.W, a.K, a.OH, a.OW, a.st, a.pad, k, c,
+                                     r, s2, b0, b1);
+            }
+        }
+        a.out2[(int64_t)bid * a.pstride + (int64_t)k * crs_n + crs] = sum;
+    }
+}
+
+template <int NF, int STEPS>
+__global__ void __launch_bounds__(256) tiny3_dw_kernel(const TinyArgs a, int pb) {
+    extern __shared__ float sm[];
+    tiny3_dw_block<NF, STEPS>(a, sm, pb, (int)gridDim.x, blockIdx.x);
+}
+
+// Both backward passes in one launch: blocks [0, ndx) are dX, the rest dW
+// partials.
+template <int KB, int ST, int NF, int STEPS>
+__global__ void __launch_bounds__(256)
+    tiny3_bwd_kernel(const TinyArgs a, const float *__restrict__ w, int ndx, int pbx, int pbw) {
+    extern __shared__ float sm[];
+    if ((int)blockIdx.x < ndx)
+        tiny3_dx_block<KB, ST>(a, w, sm, pbx, blockIdx.x);
+    else
+        tiny3_dw_block<NF, STEPS>(a, sm, pbw, (int)gridDim.x - ndx, blockIdx.x - ndx);
+}
+
 }  // namespace katsu

@@ -269,6 +269,11 @@ def test_stem_filter_gradient(xs, dev):
     ((2, 2, 9, 11), (5, 2, 3, 2), 2, 1),      # stride 2, rectangular filter
     ((3, 4, 7, 6), (16, 4, 2, 2), 1, 2),      # padding wider than the filter overhang
     ((1, 1, 5, 5), (3, 1, 5, 5), 3, 2),
+    ((1, 3, 224, 224), (8, 3, 3, 3), 2, 1),   # 3x3 register forms: stride 2
+    ((2, 4, 17, 13), (16, 4, 3, 3), 2, 1),    # 16 outputs, 4 channels, odd sizes
+    ((3, 1, 30, 70), (4, 1, 3, 3), 1, 0),     # 4 outputs, 1 channel, no padding
+    ((2, 2, 20, 19), (7, 2, 3, 3), 1, 2),     # padding past the filter overhang
+    ((600, 1, 8, 8), (2, 1, 3, 3), 1, 1),     # more dW tiles than dW blocks
 ])
 def test_few_channel_bit_exact(xs, ws, st, p, dev):
     """Layers with at most 4 input and 16 output channels run on the vector
