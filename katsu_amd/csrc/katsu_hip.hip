@@ -1470,7 +1470,7 @@ int tiny_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStr
 template <int ST>
 int tiny3_dx_launch_st(const TinyArgs &a, const float *w, const ConvDims &d, hipStream_t st) {
     const int64_t pb = cdiv((int64_t)d.H * d.W, 256);
-    const dim3 grid((unsigned)(d.C * d.N * pb));
+    const dim3 grid((unsigned)((KATSU_TINY3_DX_ALLC ? 1 : d.C) * d.N * pb));
     switch (tiny_kb(d)) {
         case 4: tiny3_dx_kernel<4, ST><<<grid, dim3(256), 0, st>>>(a, w, (int)pb); break;
         case 8: tiny3_dx_kernel<8, ST><<<grid, dim3(256), 0, st>>>(a, w, (int)pb); break;
@@ -1499,7 +1499,7 @@ template <int KB, int ST, int NF>
 int tiny3_bwd_launch_t(const TinyArgs &a, const float *w, const ConvDims &d, int64_t dwblocks,
                        size_t lds, hipStream_t st) {
     const int64_t pbx = cdiv((int64_t)d.H * d.W, 256);
-    const int64_t ndx = (int64_t)d.C * d.N * pbx;
+    const int64_t ndx = (int64_t)(KATSU_TINY3_DX_ALLC ? 1 : d.C) * d.N * pbx;
     if (ndx + dwblocks > kI32Max) return KATSU_E_INVALID;
     tiny3_bwd_kernel<KB, ST, NF, KATSU_TINY3_STEPS>
         <<<dim3((unsigned)(ndx + dwblocks)), dim3(256), lds, st>>>(a, w, (int)ndx, (int)pbx,
@@ -2039,9 +2039,9 @@ int conv_bwd_dev(const float *x, const float *w, const float *gy, float *dx, flo
             a.rows_per_block = (int)tp.rows_per_block;
             a.xw = (int)tp.xw;
             a.pstride = tp.pstride;
-            if (tiny3_ok(d))
+            if (tiny3_ok(d)) {
                 rc = tiny3_bwd_launch(a, w, d, tp, st);
-            else {
+            } else {
                 const int64_t ndx = (int64_t)d.N * d.H;
                 const size_t lds = std::max((size_t)tiny_dx_lds(d), tp.lds);
                 tiny_bwd_kernel<<<dim3((unsigned)(ndx + tp.blocks)), dim3(256), lds, st>>>(

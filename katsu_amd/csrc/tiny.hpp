@@ -22,6 +22,8 @@
 //                    this one lies within the f32 summation bound of it.
 #pragma once
 
+#include <type_traits>
+
 #include "direct.hpp"
 
 namespace katsu {
@@ -505,11 +507,126 @@ __device__ __forceinline__ void tiny3_dx_block(const TinyArgs &a, const float *_
     *dp = a.beta == 0.f ? acc : *dp + acc;
 }
 
+// dX with every input channel per thread: thread = input pixel p of image
+// b / pb (pixels [256*(b % pb), +256)), C accumulators, each summed in the
+// order above.  A block reads G once for all channels.  Weights go to LDS as
+// [k][r][s][4] (zeros past C and K).
+template <int KB, int ST>
+__device__ __forceinline__ void tiny3_dxa_block(const TinyArgs &a, const float *__restrict__ w,
+                                                float *wt, int pb, int bid) {
+#pragma clang fp contract(off)
+    constexpr int R = 3, S = 3, CC = kTinyC, NW = KB * R * S * CC, NL = (NW + 255) / 256;
+    int *nonfinite = reinterpret_cast<int *>(wt + NW);
+    const int t = threadIdx.x;
+    if (t == 0) *nonfinite = 0;
+    const int n = bid / pb, pblk = bid - n * pb;
+    const int crs = a.C * R * S;
+    // Weight slot e = ((k*R + r)*S + s)*CC + c; loads issued first, used
+    // after the G loads.
+    float wraw[NL];
+    bool wok[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int e = t + 256 * j;
+        const int c = e % CC, krs = e / CC, k = krs / (R * S), rs = krs - k * (R * S);
+        wok[j] = e < NW && k < a.K && c < a.C;
+        wraw[j] = w[wok[j] ? k * crs + c * (R * S) + rs : 0];
+    }
+    const int hw = a.H * a.W;
+    const int p0 = pblk * 256 + t;
+    const bool live = p0 < hw;
+    const int p = live ? p0 : hw - 1;
+    const int iy = p / a.W, ix = p - iy * a.W;
+    const int ohw = a.OH * a.OW;
+    bool rok[R], cok[S];
+    int oyo[R], oxo[S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int u = iy + a.pad - r;
+        rok[r] = u >= 0 && u % ST == 0 && u / ST < a.OH;
+        oyo[r] = (u / ST) * a.OW;
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+        const int u = ix + a.pad - s2;
+        cok[s2] = u >= 0 && u % ST == 0 && u / ST < a.OW;
+        oxo[s2] = u / ST;
+    }
+    const int64_t kohw = (int64_t)a.K * ohw;
+    const auto rg = buf_rsrc(a.g + n * kohw, (uint32_t)(kohw * 4));
+    float gv[KB][R][S];
+#pragma unroll
+    for (int k = 0; k < KB; ++k)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s2 = 0; s2 < S; ++s2) {
+                const bool v = k < a.K && rok[r] && cok[s2];
+                gv[k][r][s2] = buf_load(rg, v ? (k * ohw + oyo[r] + oxo[s2]) * 4 : kOOB);
+            }
+#pragma unroll
+    for (int j = 0; j < NL; ++j) asm volatile("" : "+v"(wraw[j]));
+    __syncthreads();  // *nonfinite = 0 is visible before any thread sets it
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int e = t + 256 * j;
+        if (e < NW) {
+            const float wv = wok[j] ? wraw[j] : 0.f;
+            wt[e] = wv;
+            if (!__builtin_isfinite(wv)) *nonfinite = 1;
+        }
+    }
+    __syncthreads();
+    const bool skip = *nonfinite != 0;
+    float acc[CC];
+#pragma unroll
+    for (int c = 0; c < CC; ++c) acc[c] = 0.f;
+    auto sum = [&](auto masked) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k >= a.K) continue;
+#pragma unroll
+            for (int r = R - 1; r >= 0; --r)
+#pragma unroll
+                for (int s2 = S - 1; s2 >= 0; --s2) {
+                    const floatx4 wv =
+                        *reinterpret_cast<const floatx4 *>(wt + ((k * R + r) * S + s2) * CC);
+                    const bool v = rok[r] && cok[s2];
+#pragma unroll
+                    for (int c = 0; c < CC; ++c) {
+                        if (c >= a.C) continue;
+                        const float prod = gv[k][r][s2] * wv[c];
+                        // Masked: an absent tap's product is replaced by +0.
+                        acc[c] = acc[c] + (decltype(masked)::value && !v ? 0.f : prod);
+                    }
+                }
+        }
+    };
+    if (skip)
+        sum(std::true_type{});
+    else
+        sum(std::false_type{});
+    if (!live) return;
+    float *dp = a.out + (int64_t)n * a.C * hw + p;
+#pragma unroll
+    for (int c = 0; c < CC; ++c) {
+        if (c >= a.C) continue;
+        dp[(int64_t)c * hw] = a.beta == 0.f ? acc[c] : dp[(int64_t)c * hw] + acc[c];
+    }
+}
+
+#ifndef KATSU_TINY3_DX_ALLC
+#define KATSU_TINY3_DX_ALLC 1  // dX threads take every input channel
+#endif
+
 template <int KB, int ST>
 __global__ void __launch_bounds__(256)
     tiny3_dx_kernel(const TinyArgs a, const float *__restrict__ w, int pb) {
-    __shared__ float wt[KB * 9 + 1];  // weights, then the non-finite flag
-    tiny3_dx_block<KB, ST>(a, w, wt, pb, blockIdx.x);
+    __shared__ float wt[KB * 9 * kTinyC + 1];  // weights, then the non-finite flag
+    if (KATSU_TINY3_DX_ALLC)
+        tiny3_dxa_block<KB, ST>(a, w, wt, pb, blockIdx.x);
+    else
+        tiny3_dx_block<KB, ST>(a, w, wt, pb, blockIdx.x);
 }
 
 // dW partials on the matrix cores: per block, dw[k][crs] = sum over its
@@ -622,8 +739,12 @@ template <int KB, int ST, int NF, int STEPS>
 __global__ void __launch_bounds__(256)
     tiny3_bwd_kernel(const TinyArgs a, const float *__restrict__ w, int ndx, int pbx, int pbw) {
     extern __shared__ float sm[];
-    if ((int)blockIdx.x < ndx)
-        tiny3_dx_block<KB, ST>(a, w, sm, pbx, blockIdx.x);
+    if ((int)blockIdx.x < ndx) {
+        if (KATSU_TINY3_DX_ALLC)
+            tiny3_dxa_block<KB, ST>(a, w, sm, pbx, blockIdx.x);
+        else
+            tiny3_dx_block<KB, ST>(a, w, sm, pbx, blockIdx.x);
+    }
     else
         tiny3_dw_block<NF, STEPS>(a, sm, pbw, (int)gridDim.x - ndx, blockIdx.x - ndx);
 }

@@ -305,6 +305,18 @@ def test_few_channel_bit_exact(xs, ws, st, p, dev):
     assert np.array_equal(dxa.cpu().numpy(), (dx0 + dx_ref).astype(np.float32)), "dX beta=1"
     _, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
     assert_within(dw.cpu().numpy(), dw_ref, dws, xs[0] * oh * ow, "few-channel dW")
+    # The dW blocks sum their own partials in a fixed tree (the 3x3 forms):
+    # the same bits on every call, and beta = 1 adds one more rounding.
+    for _ in range(3):
+        again = ops.conv2d_backward_filter(xd, gd, ws, st, p)
+        torch.cuda.synchronize()
+        assert torch.equal(again, dw), "dW differs between calls"
+    dw0 = synth.uniform(325, ws)
+    dwa = torch.from_numpy(dw0.copy()).to(dev)
+    ops.conv2d_backward_filter(xd, gd, ws, st, p, out=dwa, beta=1.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(dwa.cpu().numpy(), (dw0 + dw.cpu().numpy()).astype(np.float32)), \
+        "dW beta=1"
 
 
 def test_stem_kernels_two_channel_blocks(dev):
