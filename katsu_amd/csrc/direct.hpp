@@ -980,7 +980,56 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                 order_reads_then_mfma<WKF + RS, WKF * RS>();
             }
         };
-        if (!FULL && a.segs == 1 && a.OW >= 4) {
+        if (FULL && tg.tr == 1 && a.st == 1) {
+            // One output row at stride 1 (config 3): the lane's G and x
+            // addresses move 4 pixels per step, every tap offset an
+            // immediate, with no row or column counters in the loop.
+            const float *gp[WKF];
+#pragma unroll
+            for (int f = 0; f < WKF; ++f) gp[f] = base + arow + f * 16 * a.gpitch + lq;
+            const float *xp = base + bch + (tg.cx0 + lq);
+            const int nst = (tg.cx1 - tg.cx0) >> 2;
+            if (nst == 14) {
+                // 56-pixel rows: the steps unrolled, each read at an
+                // immediate offset from the lane's base addresses.
+                auto sfetch = [&](const int s, float (&av)[WKF], float (&b)[RS])
+                    __attribute__((always_inline)) {
+#pragma unroll
+                    for (int f = 0; f < WKF; ++f) av[f] = gp[f][4 * s];
+#pragma unroll
+                    for (int tap = 0; tap < RS; ++tap)
+                        b[tap] = xp[(tap / S) * Geo::PITCH + tap % S + 4 * s];
+                };
+                constexpr int NST = 14;
+                float a0[WKF], a1[WKF], b0[RS], b1[RS];
+                sfetch(0, a0, b0);
+                asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
+#pragma unroll
+                for (int s = 0; s < NST; s += 2) {
+                    sfetch(s + 1, a1, b1);
+                    mma(a0, b0, true);
+                    order_reads_then_mfma<WKF + RS, WKF * RS>();
+                    if (s + 2 < NST) sfetch(s + 2, a0, b0);
+                    mma(a1, b1, true);
+                    order_reads_then_mfma<WKF + RS, WKF * RS>();
+                }
+            } else {
+                auto rfetch = [&](float (&av)[WKF], float (&b)[RS], bool &ok)
+                    __attribute__((always_inline)) {
+                    ok = true;
+#pragma unroll
+                    for (int f = 0; f < WKF; ++f) {
+                        av[f] = *gp[f];
+                        gp[f] += 4;
+                    }
+#pragma unroll
+                    for (int tap = 0; tap < RS; ++tap)
+                        b[tap] = xp[(tap / S) * Geo::PITCH + tap % S];
+                    xp += 4;
+                };
+                run(rfetch, nst);
+            }
+        } else if (!FULL && a.segs == 1 && a.OW >= 4) {
             // Tiles of whole rows whose width is not a multiple of 4: steps
             // over the tile's flattened pixels (G is stored contiguous by
             // pixel), so only the tile's last step has idle lanes.  Each lane
