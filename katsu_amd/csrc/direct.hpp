@@ -1029,6 +1029,40 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                 };
                 run(rfetch, nst);
             }
+        } else if (!FULL && a.segs == 1 && tg.np == 56 && a.OW >= 4) {
+            // 56-pixel tiles of whole rows (config 4a: 4 rows of 14) over
+            // flattened pixels: 14 steps, every lane valid.  The lane's x
+            // offset of each step (its pixel's row and column) is computed
+            // once per tile, and its G reads take immediate offsets.
+            constexpr int NST = 14;
+            int xo[NST];
+#pragma unroll
+            for (int s = 0; s < NST; ++s) {
+                const int q = 4 * s + lq, row = q / a.OW, col = q - row * a.OW;
+                xo[s] = (row * Geo::PITCH + col) * a.st;
+            }
+            const float *gp = base + arow + lq;
+            const float *xb = base + bch;
+            auto sfetch = [&](const int s, float (&av)[WKF], float (&b)[RS])
+                __attribute__((always_inline)) {
+#pragma unroll
+                for (int f = 0; f < WKF; ++f) av[f] = gp[f * 16 * a.gpitch + 4 * s];
+                const float *xs = xb + xo[s];
+#pragma unroll
+                for (int tap = 0; tap < RS; ++tap) b[tap] = xs[(tap / S) * Geo::PITCH + tap % S];
+            };
+            float a0[WKF], a1[WKF], b0[RS], b1[RS];
+            sfetch(0, a0, b0);
+            asm volatile("" ::: "memory");  // keep step 0's reads apart from step 1's
+#pragma unroll
+            for (int s = 0; s < NST; s += 2) {
+                sfetch(s + 1, a1, b1);
+                mma(a0, b0, true);
+                order_reads_then_mfma<WKF + RS, WKF * RS>();
+                if (s + 2 < NST) sfetch(s + 2, a0, b0);
+                mma(a1, b1, true);
+                order_reads_then_mfma<WKF + RS, WKF * RS>();
+            }
         } else if (!FULL && a.segs == 1 && a.OW >= 4) {
             // Tiles of whole rows whose width is not a multiple of 4: steps
             // over the tile's flattened pixels (G is stored contiguous by
