@@ -153,6 +153,12 @@ STEM_DX_CASES = [
     ((32, 3, 99, 101), (25, 3, 7, 7)),
     ((64, 4, 64, 72), (16, 4, 7, 7)),
     ((20, 1, 224, 60), (8, 1, 7, 7)),
+    # The column-GEMM form (64 output channels, 112-pixel G rows): strips of
+    # 4 G rows with their boundary rows, a clipped last row, a clipped last
+    # column.
+    ((2, 3, 224, 224), (64, 3, 7, 7)),
+    ((5, 3, 223, 224), (64, 3, 7, 7)),
+    ((3, 3, 224, 223), (64, 3, 7, 7)),
 ]
 
 
@@ -175,3 +181,32 @@ def test_stem_data_gradient(xs, ws, dev):
     assert_within(dx.cpu().numpy(), ref, sab, ws[0] * 49, f"stem dX {xs}*{ws}")
     assert_within(dx1.cpu().numpy(), dx0.astype(np.float64) + ref, sab + np.abs(dx0),
                   ws[0] * 49 + 1, f"stem dX beta=1 {xs}*{ws}")
+
+
+def test_stem_column_gemm_strip_rows(dev):
+    """The stem's dX at its full size (64 images: strips of 28 G rows):
+    every dX row that two strips share (2*28k - 3 .. 2*28k + 1), plus the
+    first and last rows, sampled against exact f64 dot products across
+    columns and channels of several images; the result is the same bit for
+    bit on every call."""
+    import torch
+
+    from katsu_amd import ops
+    from tests.parity import sample_dx
+    c = synth.CONV_CONFIGS["c5_stem"]
+    xs, ws = c["x"], c["w"]
+    w = synth.he_normal(synth.SEED_W, ws)
+    g = synth.normal(synth.SEED_G, synth.out_shape(c))
+    wd, gd = torch.from_numpy(w).to(dev), torch.from_numpy(g).to(dev)
+    dx = ops.conv2d_backward_data(gd, wd, xs, 2, 3)
+    again = ops.conv2d_backward_data(gd, wd, xs, 2, 3)
+    torch.cuda.synchronize()
+    assert torch.equal(dx, again), "stem dX differs between calls"
+    rows = [0, 1, 2, xs[2] - 2, xs[2] - 1]
+    for k in (1, 2, 3):
+        rows += list(range(2 * 28 * k - 3, 2 * 28 * k + 2))
+    pts = [(n, ch, iy, ix) for n in (0, 17, 63) for ch in range(3) for iy in rows
+           for ix in (0, 1, 2, 3, 111, 112, 200, 221, 222, 223)]
+    ref, sab = sample_dx(g, w, xs, 2, 3, pts)
+    dxh = dx.cpu().numpy()
+    assert_within(np.array([dxh[t] for t in pts]), ref, sab, 64 * 49, "stem dX strip rows")
