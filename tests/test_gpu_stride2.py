@@ -183,12 +183,12 @@ def test_stem_data_gradient(xs, ws, dev):
                   ws[0] * 49 + 1, f"stem dX beta=1 {xs}*{ws}")
 
 
-def test_stem_column_gemm_strip_rows(dev):
-    """The stem's dX at its full size (64 images: strips of 28 G rows):
-    every dX row that two strips share (2*28k - 3 .. 2*28k + 1), plus the
-    first and last rows, sampled against exact f64 dot products across
-    columns and channels of several images; the result is the same bit for
-    bit on every call."""
+def test_stem_full_size_sampled_rows(dev):
+    """The stem's dX at its full size (64 images of 224 x 224): the first
+    and last rows and the rows around every 56th (where a kernel that works
+    in bands of 28 gradient rows would join two bands), sampled against
+    exact f64 dot products across columns and channels of several images;
+    the result is the same bit for bit on every call."""
     import torch
 
     from katsu_amd import ops
