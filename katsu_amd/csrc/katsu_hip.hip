@@ -24,6 +24,7 @@
 #include "gemm.hpp"
 #include "pointwise.hpp"
 #include "smallc.hpp"
+#include "stemdx.hpp"
 #include "tiny.hpp"
 
 namespace katsu {
@@ -1751,6 +1752,62 @@ int dx_cfg(const float *gy, const float *w, float *dx, const ConvDims &d, float 
     return rc;
 }
 
+// The stem's data gradient by rolling rows (stemdx.hpp): 3 input channels,
+// 64 output channels, 7x7, stride 2, padding 3.  Bands of `rows` flattened
+// super-rows per column tile, about one wave per SIMD; one block per CU (its
+// LDS request keeps a second block off the CU, so the waves spread over all
+// SIMDs).
+#ifndef KATSU_STEM_DX
+#define KATSU_STEM_DX 1
+#endif
+#ifndef KATSU_STEM_DX_XCD_WAVES
+#define KATSU_STEM_DX_XCD_WAVES 128
+#endif
+#ifndef KATSU_STEM_DX_PF
+#define KATSU_STEM_DX_PF 8
+#endif
+#ifndef KATSU_STEM_DX_LDS
+#define KATSU_STEM_DX_LDS 98304
+#endif
+#ifndef KATSU_STEM_DX_OCC
+#define KATSU_STEM_DX_OCC 1
+#endif
+bool stem_dx(const ConvDims &d, const float *gy, const float *w, float *dx, float beta,
+             hipStream_t st, int *rc) {
+    if (!KATSU_STEM_DX || d.C != kStemDxC || d.K != kStemDxK || d.R != 7 || d.S != 7 ||
+        d.st != 2 || d.pad != 3)
+        return false;
+    const int64_t g_bytes = d.npix_out * d.K * 4, dx_bytes = d.npix_in * d.C * 4;
+    if (g_bytes >= (int64_t)kMaxBufBytes || dx_bytes >= (int64_t)kMaxBufBytes) return false;
+    StemDxArgs a;
+    a.g = gy;
+    a.w = w;
+    a.dx = dx;
+    a.N = (int)d.N;
+    a.H = (int)d.H;
+    a.W = (int)d.W;
+    a.OH = (int)d.OH;
+    a.OW = (int)d.OW;
+    a.tiles = (int)cdiv(d.OW, 16);
+    const int64_t total = (int64_t)d.N * d.OH;
+    // At most KATSU_STEM_DX_XCD_WAVES waves (one per SIMD) on each of the 8
+    // XCDs, each XCD holding whole bands.
+    const int64_t bands_max = 8 * std::max<int64_t>(1, KATSU_STEM_DX_XCD_WAVES / a.tiles);
+    a.rows = (int)cdiv(total, bands_max);
+    a.bands = (int)cdiv(total, a.rows);
+    a.wpx = (int)cdiv(a.bands, 8) * a.tiles;
+    a.g_bytes = (uint32_t)g_bytes;
+    a.dx_bytes = (uint32_t)dx_bytes;
+    a.beta = beta;
+    const int64_t blocks = 8 * cdiv(a.wpx, 4);
+    constexpr auto kern = stem_dx_kernel<KATSU_STEM_DX_PF, KATSU_STEM_DX_OCC>;
+    constexpr size_t lds = std::max<size_t>(KATSU_STEM_DX_LDS, kStemDxWFloats * sizeof(float));
+    if ((*rc = lds_optin<kern>(lds)) != KATSU_OK) return true;
+    kern<<<dim3((unsigned)blocks), dim3(256), lds, st>>>(a);
+    *rc = launch_status();
+    return true;
+}
+
 int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_conv_geom *g,
                       float beta, hipStream_t st) {
     if (!beta_ok(beta)) return KATSU_E_INVALID;
@@ -1762,6 +1819,7 @@ int conv_bwd_data_dev(const float *gy, const float *w, float *dx, const katsu_co
     int rc = KATSU_OK;
     if (dx_as_forward(d, gy, w, dx, beta, &P) && direct_fwd<1>(P, st, &rc)) return rc;
     if (dx_phases(d, gy, w, dx, beta, st, &rc)) return rc;
+    if (stem_dx(d, gy, w, dx, beta, st, &rc)) return rc;
     if (dx_superpixel(d, gy, w, dx, beta, st, &rc)) return rc;
     if (pw_ok(d)) return pw_dx(gy, w, dx, d, beta, st);
     if (tiny_ok(d)) return tiny_dx(gy, w, dx, d, beta, st);

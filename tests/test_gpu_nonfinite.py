@@ -97,7 +97,7 @@ CASES = [
     ("c3_resnet", 2),     # the generic engine (too few tiles for the direct kernels)
     ("c4a_down3x3", 16),  # stride-2 forward, phase-form dX, stride-2 dW
     ("c4b_down1x1", 4),   # 1x1 kernels (no padding)
-    ("c5_stem", 9),       # stem forward and dW, super-pixel dX
+    ("c5_stem", 9),       # stem forward, dW and rolling-row dX
     ("c1_example", 1),    # few-channel kernels
 ]
 

@@ -7,7 +7,9 @@ cases cover 14- and 15-pixel rows and input channel counts with and without
 input channels takes the phase form (every MFMA a real tap, all four output
 phases of a channel block in one block); other stride-2 layers take the
 super-pixel form (a stride-1 convolution of G over 2x2 pixel blocks, then
-scattered back).  Phase-form cases cover odd image sizes (a super-pixel's
+scattered back), except the stem's own channel counts (3 in, 64 out), which
+take the rolling-row kernel (each output row summed over its four G rows in
+the accumulators).  Phase-form cases cover odd image sizes (a super-pixel's
 second row or column outside the image), channel counts off the 16-channel
 blocks and stages, rows of exactly 16 super-pixels, tiles of 5 rows with a
 short last tile, and beta = 1.  Shapes are chosen so the planner takes these
@@ -69,10 +71,10 @@ def test_data_gradient_3x3(xs, ws, p, dev):
     assert torch.equal(dx1, dx1c + dx)
 
 
-def test_data_gradient_superpixel_stem(dev):
+def test_data_gradient_stem_half_resolution(dev):
     """7x7 stride-2 padding-3 layer with 3 input channels (the stem's shape at
-    half resolution): sampled outputs, edges and corners included, against
-    exact f64 dot products."""
+    half resolution, rolling-row kernel): sampled outputs, edges and corners
+    included, against exact f64 dot products."""
     import torch
 
     from katsu_amd import ops
@@ -153,12 +155,17 @@ STEM_DX_CASES = [
     ((32, 3, 99, 101), (25, 3, 7, 7)),
     ((64, 4, 64, 72), (16, 4, 7, 7)),
     ((20, 1, 224, 60), (8, 1, 7, 7)),
-    # The column-GEMM form (64 output channels, 112-pixel G rows): strips of
-    # 4 G rows with their boundary rows, a clipped last row, a clipped last
-    # column.
+    # The stem's own channels (3 in, 64 out: the rolling-row kernel): bands
+    # of 2 and 4 flattened super-rows whose segments start and end at image
+    # edges and inside images, a clipped last row, a clipped last column,
+    # bands of one row on small maps, a partial column tile, a 1 x 1 map.
     ((2, 3, 224, 224), (64, 3, 7, 7)),
     ((5, 3, 223, 224), (64, 3, 7, 7)),
     ((3, 3, 224, 223), (64, 3, 7, 7)),
+    ((7, 3, 20, 36), (64, 3, 7, 7)),
+    ((3, 3, 223, 35), (64, 3, 7, 7)),
+    ((2, 3, 9, 9), (64, 3, 7, 7)),
+    ((2, 3, 2, 1), (64, 3, 7, 7)),
 ]
 
 
@@ -184,10 +191,10 @@ def test_stem_data_gradient(xs, ws, dev):
 
 
 def test_stem_full_size_sampled_rows(dev):
-    """The stem's dX at its full size (64 images of 224 x 224): the first
-    and last rows and the rows around every 56th (where a kernel that works
-    in bands of 28 gradient rows would join two bands), sampled against
-    exact f64 dot products across columns and channels of several images;
+    """The stem's dX at its full size (64 images of 224 x 224): every row of
+    three images (so every band and image boundary of a kernel that works in
+    bands of rows), sampled against exact f64 dot products at the first,
+    middle and last columns of each 16-column tile edge and all channels;
     the result is the same bit for bit on every call."""
     import torch
 
@@ -202,11 +209,9 @@ def test_stem_full_size_sampled_rows(dev):
     again = ops.conv2d_backward_data(gd, wd, xs, 2, 3)
     torch.cuda.synchronize()
     assert torch.equal(dx, again), "stem dX differs between calls"
-    rows = [0, 1, 2, xs[2] - 2, xs[2] - 1]
-    for k in (1, 2, 3):
-        rows += list(range(2 * 28 * k - 3, 2 * 28 * k + 2))
+    rows = range(xs[2])
     pts = [(n, ch, iy, ix) for n in (0, 17, 63) for ch in range(3) for iy in rows
-           for ix in (0, 1, 2, 3, 111, 112, 200, 221, 222, 223)]
+           for ix in (0, 1, 31, 32, 111, 112, 191, 192, 222, 223)]
     ref, sab = sample_dx(g, w, xs, 2, 3, pts)
     dxh = dx.cpu().numpy()
     assert_within(np.array([dxh[t] for t in pts]), ref, sab, 64 * 49, "stem dX strip rows")
