@@ -310,6 +310,189 @@ __device__ __forceinline__ void gemm_block(const GemmArgs &g, int bid, int nb) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct GEMM (gemm_rd_*): a 64 x 64 block tile whose KS waves each
+// take 1/KS of K, read both operands straight from memory into MFMA operand
+// registers (no LDS stage, no barrier in the k-loop) D k-blocks of 16 ahead,
+// and add their sums through LDS once, in wave order, at the end (K is
+// KS * NKB * 16, the whole k-loop unrolled).  For a
+// problem with about one 64 x 64 tile per CU (1024^3) this keeps every SIMD
+// on one wave's MFMAs without the per-k-tile barriers of the staged kernel.
+//
+// Operand registers per k-block of 16 (step s of lane group g is
+// k = kb + 4g + s, as in gemm_block):
+//   A, TA = 0 ([i][k]): fragment a row m is i0 + 16a + m; one 16-byte load
+//      per fragment gives the lane its four steps.
+//   A, TA = 1 ([k][i]): fragment a row m is i0 + 4m + a; one 16-byte load per
+//      step gives the lane its value in all four fragments.
+//   B likewise: TB = 1 ([j][k]) column n of fragment b is j0 + 16b + n, one
+//      load per fragment; TB = 0 ([k][j]) column n is j0 + 4n + b, one load
+//      per step.
+// So a k-block is eight 16-byte loads and 64 MFMAs per wave.
+template <bool TA, bool TB, int KS, int NKB, int D>
+__device__ __forceinline__ void gemm_rd_block(const GemmArgs &g, int bid, int nb) {
+    constexpr int T = 64;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int tile = xcd_swizzle(bid, nb);
+    const int i0 = (tile % g.tiles_m) * T, j0 = (tile / g.tiles_m) * T;
+    const int kb0 = w * NKB * 16;  // K = KS * NKB * 16 (host-checked)
+
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, g.a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(g.b, g.b_bytes);
+    // Lane parts of the byte offsets (kOOB outside the matrix) and the
+    // uniform part per k-block (soffset).  Every in-range lane's address
+    // stays inside its operand, whatever soffset's range checking.
+    int va[4], vb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (!TA) {
+            const int i = i0 + 16 * q + l16;
+            va[q] = i < g.M ? (i * g.lda + 4 * g4) * 4 : kOOB;
+        } else {
+            const int i = i0 + 4 * l16;
+            va[q] = i < g.M ? ((4 * g4 + q) * g.lda + i) * 4 : kOOB;
+        }
+        if (TB) {
+            const int j = j0 + 16 * q + l16;
+            vb[q] = j < g.N ? (j * g.ldb + 4 * g4) * 4 : kOOB;
+        } else {
+            const int j = j0 + 4 * l16;
+            vb[q] = j < g.N ? ((4 * g4 + q) * g.ldb + j) * 4 : kOOB;
+        }
+    }
+    // Byte advance of one k-block: along k within a row (k-contiguous
+    // operand) or 16 rows (otherwise).
+    const int sa = TA ? 16 * g.lda * 4 : 64, sbk = TB ? 64 : 16 * g.ldb * 4;
+    const int a_k0 = TA ? kb0 * g.lda * 4 : kb0 * 4, b_k0 = TB ? kb0 * 4 : kb0 * g.ldb * 4;
+
+    // fr[slot][0][q]: A load q, fr[slot][1][q]: B load q.
+    floatx4 fr[D][2][4];
+    auto fetch = [&](int slot, int kblk) __attribute__((always_inline)) {
+        const int oa = a_k0 + kblk * sa, ob = b_k0 + kblk * sbk;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            fr[slot][0][q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[q], oa, 0));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            fr[slot][1][q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rb, vb[q], ob, 0));
+    };
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // The whole k-loop unrolled (NKB blocks): the ring of D blocks in flight
+    // is then plain data flow, and each block waits only for its own loads.
+#pragma unroll
+    for (int p = 0; p < D && p < NKB; ++p) fetch(p, p);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        floatx4 cur[2][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cur[0][q] = fr[kb % D][0][q];
+            cur[1][q] = fr[kb % D][1][q];
+        }
+        const bool refill = kb + D < NKB;
+        if (refill) fetch(kb % D, kb + D);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const float av = TA ? cur[0][s][a] : cur[0][a][s];
+                    const float bv = TB ? cur[1][b][s] : cur[1][s][b];
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[a][b], 0, 0, 0);
+                }
+        if (refill) __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // the refill
+        __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);             // then the MFMAs
+        // Nothing crosses a block boundary: the scheduler would otherwise
+        // sink each refill to the block that uses it.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Row and column of fragment (a, b), register v, this lane.
+    auto row_of = [&](int a, int v) { const int m = 4 * g4 + v; return TA ? i0 + 4 * m + a : i0 + 16 * a + m; };
+    auto col_of = [&](int b) { return TB ? j0 + 16 * b + l16 : j0 + 4 * l16 + b; };
+    auto put = [&](int a, int v, const float *val) __attribute__((always_inline)) {
+        const int i = row_of(a, v);
+        if (i >= g.M) return;
+        float *row = g.c + (int64_t)i * g.ldc;
+        if (!TB) {
+            const int j = j0 + 4 * l16;
+            if (j >= g.N) return;
+            floatx4 r = floatx4{val[0], val[1], val[2], val[3]};
+            floatx4 *d = reinterpret_cast<floatx4 *>(row + j);
+            if (g.beta != 0.f) r += *d;
+            *d = r;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = col_of(b);
+                if (j < g.N) row[j] = g.beta != 0.f ? row[j] + val[b] : val[b];
+            }
+        }
+    };
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float val[4] = {acc[a][0][v], acc[a][1][v], acc[a][2][v], acc[a][3][v]};
+                put(a, v, val);
+            }
+    } else {
+        // The waves' sums through LDS: value idx = (a*4 + v)*4 + b of wave p
+        // at part[p][idx*64 + lane]; wave w then adds, in wave order, the
+        // (a, v) groups [w*16/KS, (w+1)*16/KS) and stores them.
+        extern __shared__ float part[];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    part[(w * 64 + (a * 4 + v) * 4 + b) * 64 + lane] = acc[a][b][v];
+        __syncthreads();
+        constexpr int GPW = 16 / KS;  // (a, v) groups per wave
+#pragma unroll
+        for (int e = 0; e < GPW; ++e) {
+            const int av = w * GPW + e, a = av >> 2, v = av & 3;
+            float val[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                float t = part[(av * 4 + b) * 64 + lane];
+#pragma unroll
+                for (int p = 1; p < KS; ++p) t += part[(p * 64 + av * 4 + b) * 64 + lane];
+                val[b] = t;
+            }
+            put(a, v, val);
+        }
+    }
+}
+
+template <bool TA, bool TB, int KS, int NKB, int D, int OCC>
+__global__ void __launch_bounds__(64 * KS, OCC) gemm_rd_kernel(const GemmArgs g) {
+    gemm_rd_block<TA, TB, KS, NKB, D>(g, blockIdx.x, gridDim.x);
+}
+
+// The matmul VJP's dA (NT) and dB (TN) in one register-direct launch (see
+// gemm_vjp_kernel for the block split).
+template <int KS, int NKB, int D, int OCC>
+__global__ void __launch_bounds__(64 * KS, OCC)
+    gemm_rd_vjp_kernel(const GemmArgs nt, const GemmArgs tn, int nb0) {
+    if ((int)blockIdx.x < nb0)
+        gemm_rd_block<false, true, KS, NKB, D>(nt, blockIdx.x, nb0);
+    else
+        gemm_rd_block<true, false, KS, NKB, D>(tn, blockIdx.x - nb0, gridDim.x - nb0);
+}
+
 template <int BM, int BN, int BK_, bool TA, bool TB, int WG>
 __global__ void __launch_bounds__(256 * WG, 2 / WG) gemm_kernel(const GemmArgs g) {
     gemm_block<BM, BN, BK_, TA, TB, WG>(g, blockIdx.x, gridDim.x);

@@ -356,10 +356,81 @@ bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, i
     return true;
 }
 
+// The register-direct GEMM (gemm.hpp, gemm_rd_*): 64 x 64 tiles whose four
+// waves each take a quarter of K, for problems of about one tile per CU
+// with K = 4 * 16 * kRdNkb (1024^3).
+#ifndef KATSU_GEMM_RD
+#define KATSU_GEMM_RD 1
+#endif
+#ifndef KATSU_GEMM_RD_D
+#define KATSU_GEMM_RD_D 4
+#endif
+#ifndef KATSU_GEMM_RD_VJP_D
+#define KATSU_GEMM_RD_VJP_D 3
+#endif
+#ifndef KATSU_GEMM_RD_KS
+#define KATSU_GEMM_RD_KS 4
+#endif
+#ifndef KATSU_GEMM_RD_VJP_KS
+#define KATSU_GEMM_RD_VJP_KS 4
+#endif
+// K = 1024: KS waves of 1024 / KS each, in blocks of 16.
+constexpr int kRdK = 1024;
+constexpr int kRdKs = KATSU_GEMM_RD_KS, kRdNkb = kRdK / 16 / kRdKs;
+constexpr int kRdVjpKs = KATSU_GEMM_RD_VJP_KS, kRdVjpNkb = kRdK / 16 / kRdVjpKs;
+
+bool gemm_rd_plan(const float *a, const float *b, const float *c, int64_t M, int64_t N,
+                  int64_t K, int ta, int tb, float beta, GemmArgs *g) {
+    if (!KATSU_GEMM_RD || M % 64 || N % 64 || K != kRdK || !aligned16(a) ||
+        !aligned16(b) || !aligned16(c))
+        return false;
+    if (M * K * 4 >= (int64_t)kMaxBufBytes || K * N * 4 >= (int64_t)kMaxBufBytes ||
+        M * N >= kI32Max)
+        return false;
+    const int64_t tiles = (M / 64) * (N / 64);
+    if (tiles < 128 || tiles > 512) return false;
+    *g = GemmArgs{};
+    g->a = a;
+    g->b = b;
+    g->M = (int)M;
+    g->N = (int)N;
+    g->K = (int)K;
+    g->lda = (int)(ta ? M : K);
+    g->ldb = (int)(tb ? K : N);
+    g->ldc = (int)N;
+    g->beta = beta;
+    g->tiles_m = (int)(M / 64);
+    g->tiles_n = (int)(N / 64);
+    g->splits = 1;
+    g->kchunk = 0;  // set by the kernel's KS
+    g->a_bytes = (uint32_t)(M * K * 4);
+    g->b_bytes = (uint32_t)(K * N * 4);
+    return true;
+}
+
+template <bool TA, bool TB>
+int gemm_rd_launch(const GemmArgs &g, hipStream_t st) {
+    constexpr auto kern = gemm_rd_kernel<TA, TB, kRdKs, kRdNkb, KATSU_GEMM_RD_D, 1>;
+    constexpr size_t lds = kRdKs * 64 * 64 * 4;
+    const int rc = lds_optin<kern>(lds);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(64 * kRdKs), lds, st>>>(g);
+    return launch_status();
+}
+
 // The planned GEMM into c, with a fixed-order reduce of the partial slices
 // when K is split.
 bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, int64_t K, int ta,
                int tb, float beta, hipStream_t st, int *rc) {
+    {
+        GemmArgs g;
+        if (gemm_rd_plan(a, b, c, M, N, K, ta, tb, beta, &g)) {
+            g.c = c;
+            *rc = !ta ? (!tb ? gemm_rd_launch<false, false>(g, st) : gemm_rd_launch<false, true>(g, st))
+                      : (!tb ? gemm_rd_launch<true, false>(g, st) : gemm_rd_launch<true, true>(g, st));
+            return true;
+        }
+    }
     GemmFastPlan pl;
     if (!gemm_fast_plan(a, b, c, M, N, K, ta, tb, beta, &pl)) return false;
     GemmArgs g = pl.g;
@@ -446,6 +517,21 @@ int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, fl
     const int64_t M = (int64_t)m, N = (int64_t)n, K = (int64_t)k;
     const bool apart = da && db && (da + M * K <= db || db + K * N <= da);
     if (apart && !empty && a && b && g) {
+        GemmArgs ra, rb;
+        if (gemm_rd_plan(g, b, da, M, K, N, 0, 1, beta_a, &ra) &&
+            gemm_rd_plan(a, g, db, K, N, M, 1, 0, beta_b, &rb) &&
+            (ra.tiles_m * ra.tiles_n) % 8 == 0) {
+            ra.c = da;
+            rb.c = db;
+            const int nb0 = ra.tiles_m * ra.tiles_n, nb1 = rb.tiles_m * rb.tiles_n;
+            constexpr auto kern =
+                gemm_rd_vjp_kernel<kRdVjpKs, kRdVjpNkb, KATSU_GEMM_RD_VJP_D, 8 / kRdVjpKs>;
+            constexpr size_t lds = kRdVjpKs * 64 * 64 * 4;
+            const int rc = lds_optin<kern>(lds);
+            if (rc != KATSU_OK) return rc;
+            kern<<<dim3((unsigned)(nb0 + nb1)), dim3(64 * kRdVjpKs), lds, st>>>(ra, rb, nb0);
+            return launch_status();
+        }
         GemmFastPlan pa, pb;
         if (gemm_fast_plan(g, b, da, M, K, N, 0, 1, beta_a, &pa) &&
             gemm_fast_plan(a, g, db, K, N, M, 1, 0, beta_b, &pb) && pa.T == pb.T &&
