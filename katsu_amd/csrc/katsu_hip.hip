@@ -1887,7 +1887,7 @@ bool stem_dx(const ConvDims &d, const float *gy, const float *w, float *dx, floa
     a.beta = beta;
     const int64_t blocks = 8 * cdiv(a.wpx, 4);
     constexpr auto kern = stem_dx_kernel<KATSU_STEM_DX_PF, KATSU_STEM_DX_OCC>;
-    constexpr size_t lds = std::max<size_t>(KATSU_STEM_DX_LDS, kStemDxWFloats * sizeof(float));
+    constexpr size_t lds = std::max<size_t>(KATSU_STEM_DX_LDS, 3 * 16 * 4 * 64 * sizeof(float));
     if ((*rc = lds_optin<kern>(lds)) != KATSU_OK) return true;
     kern<<<dim3((unsigned)blocks), dim3(256), lds, st>>>(a);
     *rc = launch_status();

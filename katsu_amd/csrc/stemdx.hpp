@@ -29,7 +29,7 @@
 // no partial sum goes through memory or LDS.
 //
 // The filter is held in registers for the whole kernel (176 values a lane,
-// staged once through LDS); G comes straight from memory, lane X reading G
+// gathered once into an LDS table in fragment order); G comes straight from memory, lane X reading G
 // columns X-1 .. X+2 of four channels per k-step, PF k-steps ahead, with
 // out-of-map columns read as zero by the buffer range check.  The loop has no
 // LDS access and no barrier.
@@ -64,7 +64,6 @@ struct StemDxArgs {
 };
 
 constexpr int kStemDxK = 64, kStemDxC = 3;
-constexpr int kStemDxWFloats = kStemDxK * kStemDxC * 49;
 
 // A row that holds a non-finite value: every element stored as the fast
 // path would store it, except that a non-finite one is first recomputed over
@@ -90,8 +89,30 @@ template <int PF, int OCC>
 __global__ void __launch_bounds__(256, OCC) stem_dx_kernel(const StemDxArgs a) {
     constexpr int KG = kStemDxK / 4;  // k-steps of a G row
     static_assert(KG % PF == 0, "prefetch ring divides the k-steps");
-    extern __shared__ float wl[];     // the filter, [64][3][7][7]
-    for (int i = threadIdx.x; i < kStemDxWFloats; i += 256) wl[i] = a.w[i];
+    // The A fragments laid out in LDS as the lanes read them: entry
+    // ((f*KG + kg)*4 + dx)*64 + lane.  Each thread gathers its 48 entries
+    // from w with every load in flight at once (a load-store loop would pay
+    // one load latency per entry), then each wave reads its 176 values at
+    // consecutive addresses.
+    extern __shared__ float at[];
+    {
+        constexpr int NE = 3 * KG * 4 * 64 / 256;
+        float v[NE];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            const int entry = e * 256 + (int)threadIdx.x;
+            const int l = entry & 63, d = (entry >> 6) & 3, kg = (entry >> 8) % KG,
+                      f = (entry >> 8) / KG;
+            const int i = l & 15, kk = l >> 4, q = i >> 2, dy = i & 3;
+            const int j = 4 * f + q, px = j / 6, c = (j % 6) / 2, py = j & 1;
+            const int r = py ? 6 - 2 * dy : 5 - 2 * dy, sx = px ? 6 - 2 * d : 5 - 2 * d;
+            v[e] = (r >= 0 && sx >= 0)
+                       ? a.w[(((4 * kg + kk) * kStemDxC + c) * 7 + r) * 7 + sx]
+                       : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < NE; ++e) at[e * 256 + threadIdx.x] = v[e];
+    }
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
@@ -108,23 +129,13 @@ __global__ void __launch_bounds__(256, OCC) stem_dx_kernel(const StemDxArgs a) {
 
     // A fragments: lane l holds A[i = l%16][k = l/16], row i = 4q + dy.
     float A[3][KG][4];
-    {
-        const int i = lane & 15, kk = lane >> 4, q = i >> 2, dy = i & 3;
 #pragma unroll
-        for (int f = 0; f < 3; ++f) {
-            const int j = 4 * f + q, px = j / 6, c = (j % 6) / 2, py = j & 1;
-            const int r = py ? 6 - 2 * dy : 5 - 2 * dy;
+    for (int f = 0; f < 3; ++f)
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg)
+        for (int kg = 0; kg < KG; ++kg)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const int s = px ? 6 - 2 * d : 5 - 2 * d;
-                    A[f][kg][d] = (r >= 0 && s >= 0)
-                                      ? wl[(((4 * kg + kk) * kStemDxC + c) * 7 + r) * 7 + s]
-                                      : 0.f;
-                }
-        }
-    }
+            for (int d = 0; d < 4; ++d)
+                if (f > 0 || d < 3) A[f][kg][d] = at[((f * KG + kg) * 4 + d) * 64 + lane];
 
     const int OHW = a.OH * a.OW;
     const int X0 = 16 * t, X = X0 + (lane & 15), kq = lane >> 4;
