@@ -694,7 +694,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                     const int Y = a.fd_ow.div(p);
                     const int iy = 2 * Y + py, ix = 2 * (p - Y * a.OW) + px;
                     if (iy < a.fh && ix < a.fw)
-                        store_beta(dst + iy * a.fw + ix,
+                        store_beta_nt(dst + iy * a.fw + ix,
                                    ys[((2 * py + px) * KT + row) * Geo::YPITCH + (e >> 1)], a.beta);
                 }
         }
@@ -709,7 +709,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                 const int X = p0 + p - Y * a.OW;
                 const int iy = 2 * Y + py, ix = 2 * X + px;
                 if (iy < a.fh && ix < a.fw)
-                    store_beta(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], a.beta);
+                    store_beta_nt(dst + iy * a.fw + ix, ys[row * Geo::YPITCH + p], a.beta);
             }
         }
     } else if (a.out_vec) {
@@ -719,10 +719,9 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             if (co >= a.CO) break;
             float *dst = outb + (int64_t)co * a.OHW + p0;
             for (int c4 = lane; c4 < n4; c4 += 64) {
-                floatx4 v = *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
-                floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
-                if (a.beta != 0.f) v += *d;
-                *d = v;
+                const floatx4 v =
+                    *reinterpret_cast<const floatx4 *>(ys + row * Geo::YPITCH + c4 * 4);
+                store4_beta_nt(reinterpret_cast<floatx4 *>(dst + c4 * 4), v, a.beta);
             }
         }
     } else {
@@ -731,7 +730,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             if (co >= a.CO) break;
             float *dst = outb + (int64_t)co * a.OHW + p0;
             for (int p = lane; p < np; p += 64)
-                store_beta(dst + p, ys[row * Geo::YPITCH + p], a.beta);
+                store_beta_nt(dst + p, ys[row * Geo::YPITCH + p], a.beta);
         }
     }
 }
