@@ -820,7 +820,10 @@ struct FwdVariant {
     static constexpr int PD = PD_;   // phase form: the layer's padding
 };
 // 3x3 stride 1 (forward and data gradient): 64 x 208-pixel tiles.
-using FwdV = FwdVariant<64, 13, 8, 3, 3, 7, 64>;
+#ifndef KATSU_FWDV
+#define KATSU_FWDV 64, 13, 8, 3, 3, 7, 64
+#endif
+using FwdV = FwdVariant<KATSU_FWDV>;
 // 3x3 stride 2 forward: 64 x 64-pixel tiles, 32-float halo rows split by
 // column parity.
 #ifndef KATSU_FWD_S2_VARIANT
@@ -1289,6 +1292,14 @@ int pw_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStrea
     return pw_run<0>(a, st);
 }
 
+// Whether the 1x1 dX epilogue may write whole 2 x 4 blocks of dx (pw_block,
+// PwArgs::quad): every output pixel's stride-2 block lies inside the image
+// and a lane's pixel pair shares a row.
+int pw_quad(const ConvDims &d, const float *dx, float beta) {
+    return d.st == 2 && d.H == 2 * d.OH && d.W == 2 * d.OW && d.OW % 2 == 0 && beta == 0.f &&
+           aligned16(dx);
+}
+
 int pw_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float beta,
           hipStream_t st) {
     PwArgs a = pw_args(d, d.C, d.npix_out, d.K);
@@ -1296,6 +1307,7 @@ int pw_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float b
     a.w = w;
     a.out = dx;
     a.beta = beta;
+    a.quad = pw_quad(d, dx, beta);
     return pw_run<1>(a, st);
 }
 
@@ -1380,6 +1392,7 @@ bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *d
     ax.w = w;
     ax.out = dx;
     ax.beta = beta;
+    ax.quad = pw_quad(d, dx, beta);
     PwArgs aw = pw_args(d, d.K, d.C, d.npix_out);
     aw.x = x;
     aw.g = gy;

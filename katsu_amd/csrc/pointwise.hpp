@@ -39,6 +39,7 @@ struct PwArgs {
     int64_t split_stride;  // floats between partial slices, or 0 when writing the output
     float beta;            // out = beta*out + result when writing the output directly
     FastDiv fd_ohw, fd_ow;
+    int quad;  // MODE 1: stride 2 onto H = 2*OH, W = 2*OW, OW even, beta 0, dx 16-byte aligned
 };
 
 template <int BM>
@@ -274,6 +275,32 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     // Epilogue: fragment (a, b), register v is tile row FM*(4*lg + v) + a,
     // tile column FN*l16 + b.
     const bool direct = g.split_stride == 0;
+    if constexpr (MODE == 1 && FN == 2) {
+        if (g.quad) {
+            // A lane's two columns are output pixels (oy, ox), (oy, ox + 1)
+            // with ox even: their 2 x 2 input blocks form a 2 x 4 block of
+            // dx, written as two 16-byte stores (taps at even columns of
+            // the first row, zeros elsewhere).
+            const int j = j0 + wj0 + 2 * l16;
+            if (j < g.N) {
+                const int n = g.fd_ohw.div(j), p = j - n * g.OHW;
+                const int oy = g.fd_ow.div(p), ox = p - oy * g.OW;
+                float *col = g.out + (int64_t)n * g.x_img + (int64_t)(2 * oy) * g.W + 2 * ox;
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int i = i0 + wi0 + FM * (4 * lg + v) + a;
+                        if (i >= g.M) continue;
+                        float *blk = col + (int64_t)i * g.HW;
+                        *reinterpret_cast<floatx4 *>(blk) =
+                            floatx4{acc[a][0][v], 0.f, acc[a][1][v], 0.f};
+                        *reinterpret_cast<floatx4 *>(blk + g.W) = floatx4{0.f, 0.f, 0.f, 0.f};
+                    }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int b = 0; b < FN; ++b) {
         const int j = j0 + wj0 + FN * l16 + b;

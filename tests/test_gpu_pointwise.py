@@ -70,14 +70,18 @@ def test_pointwise_accumulate(st, dev):
         assert np.array_equal(odd, dx0[:, :, 1::2, :]), "untouched rows changed"
 
 
-def test_pointwise_zero_fill_overwrites(dev):
-    """beta = 0 writes every dX element, zeros included, over stale contents."""
+@pytest.mark.parametrize("xs", [(2, 16, 9, 9), (2, 16, 12, 12)])
+def test_pointwise_zero_fill_overwrites(xs, dev):
+    """beta = 0 writes every dX element, zeros included, over stale contents:
+    an odd image (scalar stores, blocks clipped) and an even one (whole 2 x 4
+    blocks as 16-byte stores)."""
     import torch
 
     from katsu_amd import ops
-    xs, ws, st = (2, 16, 9, 9), (8, 16, 1, 1), 2
+    ws, st = (8, 16, 1, 1), 2
+    oh, ow = (xs[2] + 1) // 2, (xs[3] + 1) // 2
     w = synth.uniform(221, ws)
-    g = synth.uniform(223, (2, 8, 5, 5))
+    g = synth.uniform(223, (2, 8, oh, ow))
     dx = torch.full(xs, float("nan"), device=dev)
     ops.conv2d_backward_data(torch.from_numpy(g).to(dev), torch.from_numpy(w).to(dev), xs, st,
                              0, out=dx)
@@ -85,3 +89,6 @@ def test_pointwise_zero_fill_overwrites(dev):
     got = dx.cpu().numpy()
     assert np.all(np.isfinite(got))
     assert np.all(got[:, :, 1::2, :] == 0) and np.all(got[:, :, :, 1::2] == 0)
+    ref = O.conv2d_backward_data(xs, w, g, st, 0)
+    sab = O.conv2d_backward_data(xs, np.abs(w), np.abs(g), st, 0)
+    assert_within(got, ref, sab, ws[0], f"dX {xs}")
