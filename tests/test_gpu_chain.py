@@ -9,8 +9,8 @@ C ABI, each against an independent reference:
   dY = dP / 12544 spread over each row
   dX, dW = backward_buffers(x, w, dY)                         (conv2d.rs:265-292)
 
-(SURVEY's config-5 chain: Katsu has no pool op, so the pool and its VJP are
-the caller's glue between two public calls.)  The matmul head and its VJP are
+(The benchmark's config-5 chain: Katsu has no pool op, so the pool and its
+VJP are the caller's glue between two public calls.)  The matmul head and its VJP are
 compared in full with the CPU oracle; the stem passes on sampled elements
 with exact f64 dot products; the pool with an f64 mean of the device's y."""
 import numpy as np
