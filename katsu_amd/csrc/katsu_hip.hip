@@ -1239,7 +1239,25 @@ PwArgs pw_args(const ConvDims &d, int64_t m, int64_t n, int64_t k) {
     a.fd_ow = fdiv(d.OW);
     a.splits = 1;
     a.kchunk = (int)((k + 31) / 32 * 32);
+    a.x_bytes = (uint32_t)std::min<int64_t>((int64_t)d.N * d.CHW * 4, kMaxBufBytes);
+    a.w_bytes = (uint32_t)std::min<int64_t>((int64_t)d.K * d.C * 4, kMaxBufBytes);
+    a.g_bytes = (uint32_t)std::min<int64_t>((int64_t)d.N * d.KOHW * 4, kMaxBufBytes);
     return a;
+}
+
+#ifndef KATSU_PW_PF
+#define KATSU_PW_PF 2  // k-tiles in flight in pw_kernel's dX and dW (1: one, through LDS stages)
+#endif
+constexpr int kPwPf = KATSU_PW_PF;
+
+// Whether the 1x1 dX and dW take the buffer-load ring (pw_block, PF > 1):
+// every operand within the buffer range, and the dX's reduction (K output
+// channels) at least PF k-tiles deep.
+bool pw_ring(const ConvDims &d) {
+    return kPwPf > 1 && cdiv(d.K, 32) >= kPwPf &&
+           (int64_t)d.N * d.CHW * 4 < (int64_t)kMaxBufBytes &&
+           (int64_t)d.N * d.KOHW * 4 < (int64_t)kMaxBufBytes &&
+           (int64_t)d.K * d.C * 4 < (int64_t)kMaxBufBytes;
 }
 
 // 64-row tiles when they still give every CU a block, else 32.
@@ -1247,14 +1265,14 @@ int pw_bm(int64_t m, int64_t n, int64_t splits) {
     return cdiv(m, 64) * cdiv(n, 64) * splits >= kMinDirectBlocks ? 64 : 32;
 }
 
-template <int MODE, int BM, int V>
+template <int MODE, int BM, int V, int PF>
 int pw_launch(PwArgs a, hipStream_t st) {
     a.tiles_m = (int)cdiv(a.M, BM);
     a.tiles_n = (int)cdiv(a.N, PwGeo<BM>::BN);
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * a.splits;
     if (blocks <= 0) return KATSU_OK;
     if (blocks > kI32Max) return KATSU_E_INVALID;
-    pw_kernel<MODE, BM, V><<<dim3((unsigned)blocks), dim3(256), PwGeo<BM>::kBytes, st>>>(a);
+    pw_kernel<MODE, BM, V, PF><<<dim3((unsigned)blocks), dim3(256), PwGeo<BM>::kBytes, st>>>(a);
     return launch_status();
 }
 
@@ -1269,18 +1287,48 @@ int pw_vec(const PwArgs &a, int mode) {
     return mode == 1 && gv ? 3 : 1;
 }
 
-template <int MODE, int V>
+template <int MODE, int V, int PF>
 int pw_run_v(const PwArgs &a, hipStream_t st) {
-    return pw_bm(a.M, a.N, a.splits) == 64 ? pw_launch<MODE, 64, V>(a, st)
-                                             : pw_launch<MODE, 32, V>(a, st);
+    return pw_bm(a.M, a.N, a.splits) == 64 ? pw_launch<MODE, 64, V, PF>(a, st)
+                                             : pw_launch<MODE, 32, V, PF>(a, st);
 }
 
-template <int MODE>
-int pw_run(const PwArgs &a, hipStream_t st) {
+template <int MODE, int PF>
+int pw_run_pf(const PwArgs &a, hipStream_t st) {
     const int v = pw_vec(a, MODE);
-    if (MODE == 1 && v == 3) return pw_run_v<MODE, MODE == 1 ? 3 : 0>(a, st);
-    if (v == 1) return pw_run_v<MODE, 1>(a, st);
-    return pw_run_v<MODE, 0>(a, st);
+    if (MODE == 1 && v == 3) return pw_run_v<MODE, MODE == 1 ? 3 : 0, PF>(a, st);
+    if (v == 1) return pw_run_v<MODE, 1, PF>(a, st);
+    return pw_run_v<MODE, 0, PF>(a, st);
+}
+
+// ring: pw_ring(d) for the layer (dX and dW only).
+template <int MODE>
+int pw_run(const PwArgs &a, bool ring, hipStream_t st) {
+    if constexpr (MODE != 0 && kPwPf > 1)
+        if (ring) return pw_run_pf<MODE, kPwPf>(a, st);
+    return pw_run_pf<MODE, 1>(a, st);
+}
+
+#ifndef KATSU_PW_RD
+#define KATSU_PW_RD 1
+#endif
+
+// The register-direct forward (pw_rd_fwd_kernel): C = 64, 128 or 256, w rows
+// 16-byte aligned, operands within the buffer range, at least one block per CU.
+template <int NKB>
+int pw_rd_fwd_launch(PwArgs a, hipStream_t st) {
+    a.tiles_m = (int)cdiv(a.M, 64);
+    a.tiles_n = (int)cdiv(a.N, 64);
+    const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
+    pw_rd_fwd_kernel<NKB><<<dim3((unsigned)blocks), dim3(256), 4 * 64 * 64 * sizeof(float), st>>>(a);
+    return launch_status();
+}
+
+bool pw_rd_fwd_ok(const ConvDims &d, const float *x, const float *w) {
+    const int64_t xb = (int64_t)d.N * d.CHW * 4, wb = (int64_t)d.K * d.C * 4;
+    return KATSU_PW_RD && (d.C == 64 || d.C == 128 || d.C == 256) && aligned16(w) &&
+           xb < (int64_t)kMaxBufBytes && wb < (int64_t)kMaxBufBytes &&
+           cdiv(d.K, 64) * cdiv(d.npix_out, 64) >= kMinDirectBlocks;
 }
 
 int pw_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st) {
@@ -1289,7 +1337,14 @@ int pw_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStrea
     a.w = w;
     a.out = y;
     a.beta = 0.f;
-    return pw_run<0>(a, st);
+    if (pw_rd_fwd_ok(d, x, w)) {
+        a.x_bytes = (uint32_t)((int64_t)d.N * d.CHW * 4);
+        a.w_bytes = (uint32_t)((int64_t)d.K * d.C * 4);
+        return d.C == 64    ? pw_rd_fwd_launch<1>(a, st)
+               : d.C == 128 ? pw_rd_fwd_launch<2>(a, st)
+                            : pw_rd_fwd_launch<4>(a, st);
+    }
+    return pw_run<0>(a, false, st);
 }
 
 // Whether the 1x1 dX epilogue may write whole 2 x 4 blocks of dx (pw_block,
@@ -1308,7 +1363,7 @@ int pw_dx(const float *gy, const float *w, float *dx, const ConvDims &d, float b
     a.out = dx;
     a.beta = beta;
     a.quad = pw_quad(d, dx, beta);
-    return pw_run<1>(a, st);
+    return pw_run<1>(a, pw_ring(d), st);
 }
 
 // dW: the pixel reduction split so the launch has about two blocks per CU,
@@ -1327,7 +1382,9 @@ PwDwPlan pw_dw_plan(const ConvDims &d) {
     const int64_t tiles = cdiv(d.K, 32) * cdiv(d.C, 64);
     int64_t splits = std::max<int64_t>(1, cdiv(2 * kMinDirectBlocks, tiles));
     splits = std::min(splits, std::max<int64_t>(1, kred / 256));
-    const int64_t kchunk = cdiv(cdiv(kred, splits), 32) * 32;
+    // With the ring, slices of whole rounds of kPwPf k-tiles.
+    const int64_t q = pw_ring(d) ? 32 * kPwPf : 32;
+    const int64_t kchunk = cdiv(cdiv(kred, splits), q) * q;
     splits = cdiv(kred, kchunk);
     pl.ok = true;
     pl.splits = (int)splits;
@@ -1348,7 +1405,7 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
     a.splits = pl.splits;
     a.kchunk = pl.kchunk;
     a.split_stride = direct ? 0 : pl.pstride;
-    const int rc = pw_run<2>(a, st);
+    const int rc = pw_run<2>(a, pw_ring(d), st);
     if (rc != KATSU_OK || direct) return rc;
     return launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
 }
@@ -1357,7 +1414,7 @@ int pw_dw(const float *x, const float *gy, float *dw, const ConvDims &d, const P
 // the same plans as the two separate calls, so the same bits.  False = the
 // dW block count is not a multiple of 8 (the shared grid would move the dX
 // blocks' XCD placement): the caller runs the separate calls.
-template <int BMX, int BMW, int VX, int VW>
+template <int BMX, int BMW, int VX, int VW, int PF>
 int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     ax.tiles_m = (int)cdiv(ax.M, BMX);
     ax.tiles_n = (int)cdiv(ax.N, PwGeo<BMX>::BN);
@@ -1366,22 +1423,31 @@ int pw_bwd_launch(PwArgs ax, PwArgs aw, hipStream_t st) {
     const int64_t bx = (int64_t)ax.tiles_m * ax.tiles_n, bw = (int64_t)aw.tiles_m * aw.tiles_n * aw.splits;
     if (bx + bw > kI32Max) return KATSU_E_INVALID;
     const size_t lds = std::max(PwGeo<BMX>::kBytes, PwGeo<BMW>::kBytes);
-    pw_bwd_kernel<BMX, BMW, VX, VW><<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
+    pw_bwd_kernel<BMX, BMW, VX, VW, PF>
+        <<<dim3((unsigned)(bx + bw)), dim3(256), lds, st>>>(ax, aw, (int)bw);
     return launch_status();
 }
 
-template <int VX, int VW>
+template <int VX, int VW, int PF>
 int pw_bwd_bm(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
-    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, VX, VW>(ax, aw, st)
-                                  : pw_bwd_launch<64, 32, VX, VW>(ax, aw, st))
-                     : (bmw == 64 ? pw_bwd_launch<32, 64, VX, VW>(ax, aw, st)
-                                  : pw_bwd_launch<32, 32, VX, VW>(ax, aw, st));
+    return bmx == 64 ? (bmw == 64 ? pw_bwd_launch<64, 64, VX, VW, PF>(ax, aw, st)
+                                  : pw_bwd_launch<64, 32, VX, VW, PF>(ax, aw, st))
+                     : (bmw == 64 ? pw_bwd_launch<32, 64, VX, VW, PF>(ax, aw, st)
+                                  : pw_bwd_launch<32, 32, VX, VW, PF>(ax, aw, st));
 }
 
-template <int VX>
+template <int VX, int PF>
 int pw_bwd_vw(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
-    return pw_vec(aw, 2) == 1 ? pw_bwd_bm<VX, 1>(bmx, bmw, ax, aw, st)
-                              : pw_bwd_bm<VX, 0>(bmx, bmw, ax, aw, st);
+    return pw_vec(aw, 2) == 1 ? pw_bwd_bm<VX, 1, PF>(bmx, bmw, ax, aw, st)
+                              : pw_bwd_bm<VX, 0, PF>(bmx, bmw, ax, aw, st);
+}
+
+template <int PF>
+int pw_bwd_pf(int bmx, int bmw, const PwArgs &ax, const PwArgs &aw, hipStream_t st) {
+    const int vx = pw_vec(ax, 1);
+    return vx == 3   ? pw_bwd_vw<3, PF>(bmx, bmw, ax, aw, st)
+           : vx == 1 ? pw_bwd_vw<1, PF>(bmx, bmw, ax, aw, st)
+                     : pw_bwd_vw<0, PF>(bmx, bmw, ax, aw, st);
 }
 
 bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *dw,
@@ -1404,10 +1470,8 @@ bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *d
     aw.split_stride = direct ? 0 : pl.pstride;
     const int bmx = pw_bm(ax.M, ax.N, 1), bmw = pw_bm(aw.M, aw.N, aw.splits);
     if (cdiv(aw.M, bmw) * cdiv(aw.N, 64) * aw.splits % 8 != 0) return false;
-    const int vx = pw_vec(ax, 1);
-    *rc = vx == 3   ? pw_bwd_vw<3>(bmx, bmw, ax, aw, st)
-          : vx == 1 ? pw_bwd_vw<1>(bmx, bmw, ax, aw, st)
-                    : pw_bwd_vw<0>(bmx, bmw, ax, aw, st);
+    *rc = pw_ring(d) ? pw_bwd_pf<kPwPf>(bmx, bmw, ax, aw, st)
+                     : pw_bwd_pf<1>(bmx, bmw, ax, aw, st);
     if (*rc == KATSU_OK && !direct)
         *rc = launch_split_reduce(ws, dw, (int64_t)d.K * d.C, pl.pstride, pl.splits, beta, st);
     return true;

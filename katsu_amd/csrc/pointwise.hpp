@@ -40,6 +40,7 @@ struct PwArgs {
     float beta;            // out = beta*out + result when writing the output directly
     FastDiv fd_ohw, fd_ow;
     int quad;  // MODE 1: stride 2 onto H = 2*OH, W = 2*OW, OW even, beta 0, dx 16-byte aligned
+    uint32_t x_bytes, w_bytes, g_bytes;  // buffer-resource sizes (buffer-load forms)
 };
 
 template <int BM>
@@ -58,7 +59,15 @@ struct PwGeo {
 // in MODE 2: OH*OW % 4 = 0, G 16-byte aligned); V = 3 also G 16 bytes at a
 // time in MODE 1 (same condition), each thread then taking four adjacent
 // pixel columns.
-template <int MODE, int BM, int V>
+// A value the compiler may not reason about: a buffer offset selected
+// between an address and kOOB stays one unconditional load, instead of
+// being split into a branch around the load.
+__device__ __forceinline__ int vopaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+template <int MODE, int BM, int V, int PF = 1>
 __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     constexpr bool AV = (V & 1) != 0, BV = MODE == 1 && (V & 2) != 0;
     using Geo = PwGeo<BM>;
@@ -253,7 +262,130 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
             }
     };
 
-    if (kb < ke) {
+    if constexpr (PF > 1) {
+        // Buffer loads with PF k-tiles in flight (MODE 1 and 2): tile t's
+        // registers are stored to LDS stage t % 2 and refilled with tile
+        // t + PF before tile t's MFMAs.  Every load is issued whatever k
+        // (kOOB past the slice, reading zeros), so the loop is the same on
+        // every pass and each store waits only for its own tile; the k-tiles
+        // past the slice's end up to a multiple of PF add zeros.
+        static_assert(MODE != 0 && PF % 2 == 0, "ring: dX and dW, an even depth");
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.w, g.w_bytes);
+        const __amdgpu_buffer_rsrc_t rgg = buf_rsrc(g.g, g.g_bytes);
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(g.x, g.x_bytes);
+        auto bload = [&](int k0, float (&xa)[NA], float (&xb)[NB])
+                         __attribute__((always_inline)) {
+            if (MODE == 1) {
+                // A: w[o = k][c = i], four channels per 16-byte load (AV).
+                if (AV) {
+#pragma unroll
+                    for (int q = 0; q < NA / 4; ++q) {
+                        const int e = q * 256 + tid;
+                        const int i = i0 + 4 * (e % (BM / 4)), k = k0 + e / (BM / 4);
+                        const int off = vopaque((i < g.M && k < ke) ? (k * g.C + i) * 4 : kOOB);
+                        const floatx4 v = __builtin_bit_cast(
+                            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) xa[4 * q + r] = v[r];
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NA; ++q) {
+                        const int e = q * 256 + tid;
+                        const int i = i0 + e % BM, k = k0 + e / BM;
+                        const int off = vopaque((i < g.M && k < ke) ? (k * g.C + i) * 4 : kOOB);
+                        xa[q] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rw, off, 0, 0));
+                    }
+                }
+                // B: G[n][o = k][p], four pixels per 16-byte load (BV).
+                if (BV) {
+#pragma unroll
+                    for (int q = 0; q < NB / 4; ++q) {
+                        const int k = k0 + q * 16 + (tid >> 4);
+                        const int off = vopaque((colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
+                        const floatx4 v = __builtin_bit_cast(
+                            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rgg, off, 0, 0));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) xb[4 * q + r] = v[r];
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NB; ++q) {
+                        const int k = k0 + q * 4 + (tid >> 6);
+                        const int off = vopaque((colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
+                        xb[q] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rgg, off, 0, 0));
+                    }
+                }
+            } else {
+                // One pixel per thread per k-tile, k = k0 + tid % 32.
+                const int k = k0 + (tid & (BK - 1));
+                const bool kok = k < ke;
+                const int kk = kok ? k : 0;
+                const int n = g.fd_ohw.div(kk);
+                const int p = kk - n * g.OHW;
+                const int oy = g.fd_ow.div(p);
+                const int ox = p - oy * g.OW;
+                const int gb = (int)((int64_t)n * g.g_img + p);
+                const int xb0 = (int)((int64_t)n * g.x_img + (int64_t)(oy * g.W + ox) * g.st);
+                if (AV) {  // G[n][o][p..p+3]: pixels k4 .. k4+3 of one image
+                    const int k4 = k0 + 4 * (tid & (BK / 4 - 1));
+                    const bool k4ok = k4 < ke;
+                    const int kk4 = k4ok ? k4 : 0;
+                    const int n4 = g.fd_ohw.div(kk4);
+                    const int gb4 = (int)((int64_t)n4 * g.g_img + (kk4 - n4 * g.OHW));
+#pragma unroll
+                    for (int q = 0; q < NA / 4; ++q) {
+                        const int i = i0 + q * (1024 / BK) + (tid / (BK / 4));
+                        const int off = vopaque((k4ok && i < g.M) ? (gb4 + i * g.OHW) * 4 : kOOB);
+                        const floatx4 v = __builtin_bit_cast(
+                            floatx4, __builtin_amdgcn_raw_buffer_load_b128(rgg, off, 0, 0));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) xa[4 * q + r] = v[r];
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NA; ++q) {  // G[n][o][p]
+                        const int i = i0 + q * (256 / BK) + (tid / BK);
+                        const int off = vopaque((kok && i < g.M) ? (gb + i * g.OHW) * 4 : kOOB);
+                        xa[q] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rgg, off, 0, 0));
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < NB; ++q) {  // x[n][c][oy*s][ox*s]
+                    const int j = j0 + q * (256 / BK) + (tid / BK);
+                    const int off = vopaque((kok && j < g.N) ? (xb0 + j * g.HW) * 4 : kOOB);
+                    xb[q] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+                }
+            }
+        };
+        if (kb < ke) {
+            const int T = (ke - kb + BK - 1) / BK;
+            float ra[PF][NA], rb[PF][NB];
+#pragma unroll
+            for (int d = 0; d < PF; ++d) bload(kb + d * BK, ra[d], rb[d]);
+            for (int t0 = 0; t0 < T; t0 += PF) {
+#pragma unroll
+                for (int d = 0; d < PF; ++d) {
+                    float *stg = smem + (d & 1) * Geo::STAGE;
+#pragma unroll
+                    for (int q = 0; q < NA; ++q) va[q] = ra[d][q];
+#pragma unroll
+                    for (int q = 0; q < NB; ++q) vb[q] = rb[d][q];
+                    store(stg);
+                    __syncthreads();
+                    bload(kb + (t0 + d + PF) * BK, ra[d], rb[d]);
+                    // The refill is issued before the tile's LDS reads and MFMAs.
+                    __builtin_amdgcn_sched_barrier(0);
+                    compute(stg);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+    } else if (kb < ke) {
         float *st0 = smem, *st1 = smem + Geo::STAGE;
         load(kb);
         store(st0);
@@ -356,22 +488,135 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     }
 }
 
-template <int MODE, int BM, int V>
+// The forward of a 1x1 layer whose input channels split into four 16-deep
+// multiples (C = 64 * NKB), register-direct: a block is one 64 x 64 tile of
+// (output channel, output pixel), and wave w takes input channels
+// [16 NKB w, 16 NKB (w + 1)).  Each wave loads its operands straight into
+// MFMA operand registers, every load of its k-range in flight at once (no LDS
+// stage, no barrier before the epilogue):
+//   A = w[o][c], c contiguous: one 16-byte load per 16-row fragment gives a
+//       lane w[o][c0 + 4 g4 .. +3], its four k-steps (lane group g4 = l/16);
+//   B = x[n][c][oy s][ox s]: fragment b is output pixels j0 + 16 b + l%16,
+//       one 4-byte load per k-step, channel c0 + 4 g4 + step.
+// So MFMA k-row g4 of step s is channel c0 + 4 g4 + s in both operands.  The
+// four waves' sums go through LDS and are added in wave order; wave w then
+// stores output channels i0 + 16 w .. +15, a row of 64 consecutive pixels per
+// store.
+template <int NKB>
+__device__ __forceinline__ void pw_rd_fwd_block(const PwArgs &g, int bid, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int tile = xcd_swizzle(bid, nb);
+    const int i0 = (tile % g.tiles_m) * 64, j0 = (tile / g.tiles_m) * 64;
+    const int c0 = w * NKB * 16;
+
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.w, g.w_bytes);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(g.x, g.x_bytes);
+    // Lane parts of the byte offsets (kOOB past the last row or pixel).
+    int vw[4], vx[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = i0 + 16 * q + l16;
+        vw[q] = i < g.M ? (i * g.C + 4 * g4) * 4 : kOOB;
+        const int j = j0 + 16 * q + l16;
+        if (j < g.N) {
+            const int n = g.fd_ohw.div(j), p = j - n * g.OHW;
+            const int oy = g.fd_ow.div(p), ox = p - oy * g.OW;
+            vx[q] = (int)((int64_t)n * g.x_img + (int64_t)(oy * g.W + ox) * g.st +
+                          (int64_t)4 * g4 * g.HW) * 4;
+        } else {
+            vx[q] = kOOB;
+        }
+    }
+    const int hw4 = g.HW * 4;
+
+    floatx4 fa[NKB][4];
+    float fb[NKB][4][4];  // [k-block][fragment][step]
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        const int c = c0 + 16 * kb;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            fa[kb][q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[q], c * 4, 0));
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                fb[kb][q][s] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rx, vx[q], (c + s) * hw4, 0));
+    }
+    // Every load issued before the first MFMA: left alone, the scheduler
+    // sinks each load to its first use and waits for it there.
+    __builtin_amdgcn_sched_barrier(0);
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[kb][a][s], fb[kb][b][s],
+                                                                     acc[a][b], 0, 0, 0);
+
+    // Value (a, b, v) of wave p (tile row 16a + 4 g4 + v, column 16b + l16) at
+    // part[p][((a*4 + v)*4 + b)*64 + 16 (g4 ^ b) + l16]: the xor puts both the
+    // writes (fixed b) and the reads (fixed g4) of a wave on 64 distinct words.
+    extern __shared__ float part[];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                part[(w * 64 + (a * 4 + v) * 4 + b) * 64 + ((g4 ^ b) << 4) + l16] = acc[a][b][v];
+    __syncthreads();
+    const int j = j0 + lane;
+    if (j >= g.N) return;
+    const int n = g.fd_ohw.div(j), p = j - n * g.OHW;
+    float *col = g.out + (int64_t)n * g.g_img + p;
+    const int b = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = i0 + 16 * w + r;
+        if (i >= g.M) break;
+        const int v = r & 3, rg = r >> 2;  // row r = 4 rg + v of fragment a = w
+        const int idx = ((w * 4 + v) * 4 + b) * 64 + ((rg ^ b) << 4) + l16;
+        float t = part[idx];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) t += part[q * 64 * 64 + idx];
+        col[(int64_t)i * g.OHW] = t;
+    }
+}
+
+template <int NKB>
+__global__ void __launch_bounds__(256, 2) pw_rd_fwd_kernel(const PwArgs g) {
+    pw_rd_fwd_block<NKB>(g, blockIdx.x, gridDim.x);
+}
+
+template <int MODE, int BM, int V, int PF>
 __global__ void __launch_bounds__(256, 2) pw_kernel(const PwArgs g) {
-    pw_block<MODE, BM, V>(g, blockIdx.x, gridDim.x);
+    pw_block<MODE, BM, V, PF>(g, blockIdx.x, gridDim.x);
 }
 
 // dX and the dW partials of a 1x1 layer in one launch (conv2d.rs:265-292):
 // blocks [0, nbw) are dW blocks (the longer ones, dispatched first), the
 // rest dX blocks; nbw is a multiple of 8, so each pass keeps its XCD
 // placement.
-template <int BMX, int BMW, int VX, int VW>
+template <int BMX, int BMW, int VX, int VW, int PF>
 __global__ void __launch_bounds__(256, 2) pw_bwd_kernel(const PwArgs dx, const PwArgs dw,
                                                         int nbw) {
     if ((int)blockIdx.x < nbw)
-        pw_block<2, BMW, VW>(dw, blockIdx.x, nbw);
+        pw_block<2, BMW, VW, PF>(dw, blockIdx.x, nbw);
     else
-        pw_block<1, BMX, VX>(dx, blockIdx.x - nbw, gridDim.x - nbw);
+        pw_block<1, BMX, VX, PF>(dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
 }  // namespace katsu

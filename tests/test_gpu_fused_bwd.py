@@ -32,6 +32,7 @@ CASES = [
     ((2, 16, 12, 12), (8, 16, 1, 1), 1, 0, False),     # 1x1
     ((32, 128, 28, 28), (256, 128, 1, 1), 2, 0, False),  # config 4b: one pw_bwd_kernel launch
     ((6, 40, 15, 17), (24, 40, 1, 1), 2, 0, False),    # 1x1 stride 2, odd sizes
+    ((16, 40, 30, 32), (64, 40, 1, 1), 1, 0, False),   # 1x1 stride 1, 240 dW slices
     ((1, 3, 224, 224), (8, 3, 3, 3), 1, 1, False),     # config 1: few-channel register forms
     ((2, 4, 17, 13), (16, 4, 3, 3), 2, 1, False),      # few channels, stride 2
     ((600, 1, 8, 8), (2, 1, 3, 3), 1, 1, False),       # more dW tiles than dW blocks

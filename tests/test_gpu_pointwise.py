@@ -3,7 +3,9 @@
 These layers take the pointwise GEMM path for all three passes: the forward
 gathers input pixel (oy*s, ox*s), dX writes each output pixel's value at the
 corner of the s x s input block it owns and zeros in the rest of the block,
-and dW sums over every output pixel with a fixed split order.  Cases cover
+and dW sums over every output pixel with a fixed split order.  With 64, 128
+or 256 input channels and a block per CU the forward is register-direct
+(pw_rd_fwd_kernel: operands loaded straight into MFMA registers).  Cases cover
 strides 1-3 (blocks clipped at the image edge), channel counts off the 32-
 and 64-wide tiles, pixel tiles that straddle images, the split dW, and
 beta = 1 accumulation (the zero positions of dX are left as they were)."""
@@ -25,6 +27,17 @@ CASES = [
     ((4, 128, 28, 28), (256, 128, 1, 1), 2),  # config 4b's layer on 4 images
     ((16, 32, 32, 32), (64, 32, 1, 1), 1),    # long pixel reduction: split dW
     ((1, 1, 1, 1), (1, 1, 1, 1), 1),
+    # Register-direct forward (64, 128 or 256 input channels, a block per CU
+    # at least): config 4b at full size; 64 channels with a partial output
+    # channel block and pixel tiles straddling images; 256 channels at
+    # stride 2 with a partial last pixel tile.
+    ((32, 128, 28, 28), (256, 128, 1, 1), 2),
+    ((16, 64, 30, 30), (130, 64, 1, 1), 1),
+    ((24, 256, 40, 42), (70, 256, 1, 1), 2),
+    # Full-size grids for the tiled backward: 40 input channels (a partial
+    # 64-wide dW tile), and 256 channels onto whole stride-2 blocks.
+    ((16, 40, 30, 32), (64, 40, 1, 1), 1),
+    ((32, 256, 28, 28), (64, 256, 1, 1), 2),
 ]
 
 
@@ -38,14 +51,17 @@ def test_pointwise_parity(xs, ws, st, dev):
     _check_full(x, w, g, st, 0, dev, f"{xs}*{ws} s{st}")
 
 
-@pytest.mark.parametrize("st", [1, 2])
-def test_pointwise_accumulate(st, dev):
+@pytest.mark.parametrize("st,xs,ws", [(1, (3, 40, 11, 12), (24, 40, 1, 1)),
+                                      (2, (3, 40, 11, 12), (24, 40, 1, 1)),
+                                      (1, (16, 40, 30, 32), (64, 40, 1, 1)),
+                                      (1, (1, 8, 4, 4), (8, 8, 1, 1))])
+def test_pointwise_accumulate(st, xs, ws, dev):
     """beta = 1: dX and dW add into what the buffers hold; with stride 2 the
-    input pixels no tap reaches keep their old values."""
+    input pixels no tap reaches keep their old values.  The last case has one
+    dW slice, written straight into dw."""
     import torch
 
     from katsu_amd import ops
-    xs, ws = (3, 40, 11, 12), (24, 40, 1, 1)
     x = synth.uniform(211, xs)
     w = synth.uniform(212, ws)
     oh, ow = (xs[2] - 1) // st + 1, (xs[3] - 1) // st + 1
