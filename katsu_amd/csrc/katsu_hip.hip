@@ -1483,14 +1483,23 @@ bool pw_bwd(const float *x, const float *w, const float *gy, float *dx, float *d
 
 constexpr int kStemF = 7, kStemPitch = 256;
 
+template <int ST>
+int stem_fwd_launch(const StemArgs &a, unsigned blocks, hipStream_t st) {
+    using Geo = StemGeo<3, 7, 7, kStemPitch>;
+    constexpr auto kern = stem_fwd_kernel<3, 7, 7, kStemF, kStemPitch, ST>;
+    const int rc = lds_optin<kern>(Geo::kBytes);
+    if (rc != KATSU_OK) return rc;
+    kern<<<dim3(blocks), dim3(512), Geo::kBytes, st>>>(a);
+    return launch_status();
+}
+
 bool stem_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipStream_t st,
               int *rc) {
     using Geo = StemGeo<3, 7, 7, kStemPitch>;
     if (d.C != 3 || d.R != 7 || d.S != 7) return false;
-    // Whole rows of 64..112 pixels; the padded tap s = 7 reads one column
-    // past the halo, which must still lie inside the row pitch.
-    if (d.OW < 64 || d.OW > 16 * kStemF || (int64_t)(d.OW - 1) * d.st + Geo::SP > kStemPitch)
-        return false;
+    // Whole rows of 64..112 pixels, stride 1 or 2 (every lane's halo columns,
+    // 16*kStemF of them, then fit the row pitch).
+    if (d.OW < 64 || d.OW > 16 * kStemF || d.st > 2) return false;
     if ((int64_t)d.CHW * 4 >= (int64_t)kMaxBufBytes ||
         (int64_t)d.K * d.CRS * 4 >= (int64_t)kMaxBufBytes)
         return false;
@@ -1521,10 +1530,8 @@ bool stem_fwd(const float *x, const float *w, float *y, const ConvDims &d, hipSt
     a.co_blocks = (int)co_blocks;
     a.ncols = (d.OW - 1) * d.st + d.S;
     a.w_bytes = (uint32_t)((int64_t)d.K * d.CRS * 4);
-    constexpr auto kern = stem_fwd_kernel<3, 7, 7, kStemF, kStemPitch>;
-    if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
-    kern<<<dim3((unsigned)blocks), dim3(512), Geo::kBytes, st>>>(a);
-    *rc = launch_status();
+    *rc = d.st == 2 ? stem_fwd_launch<2>(a, (unsigned)blocks, st)
+                    : stem_fwd_launch<1>(a, (unsigned)blocks, st);
     return true;
 }
 

@@ -4,16 +4,16 @@
 // w[o][c][r][s] * x[c][oy*st - pad + r][ox*st - pad + s].
 //
 // GEMM view: i = output channel (64 per block), j = output pixel (one image
-// row per step), k = (c, r, s) with s padded to 8.  A k-step of four takes
-// taps s = 4h .. 4h+3 of one (c, r), lane group lg (lanes 16lg..16lg+15)
-// taking s = 4h + lg.  Every LDS address is then a per-lane base (the lane's
-// pixel column plus lg) plus a compile-time step offset; the lane groups of a
-// stride-2 read fall on distinct banks; and the padding costs 8/7 of the
-// MFMAs (three channels in quads, as the general direct kernel stages them,
-// would cost 4/3).
+// row per step), k = (c, r, s) in the filter's own order, padded from 147 to
+// 148.  k-step t takes k = 4t .. 4t+3, lane group lg (lanes 16lg..16lg+15)
+// taking k = 4t + lg; the lane's halo offset of that tap is a per-lane
+// register (the four taps of a step can straddle filter rows), so a B read is
+// the lane's pixel column plus that offset.  37 k-steps per row: the padding
+// costs 148/147 of the MFMAs (s padded to 8 would cost 8/7, three channels in
+// quads, as the general direct kernel stages them, 4/3).
 //
 // A block is 512 threads: two groups of four waves that share the filter in
-// LDS (64 x 3*7*8 floats, staged once) and each walk their own output rows
+// LDS (64 x 148 floats, staged once) and each walk their own output rows
 // (group g takes rows r0 + g, r0 + g + 2, ...) through a double-buffered
 // halo of 7 input rows per channel.  Wave q of a group owns output channels
 // 16q .. 16q+15 and the whole row (F fragments of 16 pixels).  A row's output
@@ -39,22 +39,23 @@ struct StemArgs {
 
 template <int CC, int R, int S, int PITCH>
 struct StemGeo {
-    static constexpr int SP = 8;                 // s padded to two halves of four
-    static constexpr int WK = CC * R * SP;       // k extent of a filter row
+    static constexpr int CRS = CC * R * S;
+    static constexpr int WK = (CRS + 3) / 4 * 4;  // k extent of a filter row: (c, r, s) flat
     static constexpr int WP = WK + 2;            // == 2 (mod 4): a half-wave's A reads on 32 banks
     static constexpr int WS = (64 * WP + 255) / 256 * 256;
     static constexpr int CP = R * PITCH;         // halo channel pitch
     static constexpr int HS = CC * CP;           // one halo stage
     static constexpr int TOTAL = WS + 4 * HS;    // filter + two groups x two stages
     static constexpr size_t kBytes = (size_t)TOTAL * sizeof(float);
-    static_assert(S <= SP && PITCH % 64 == 0, "stem geometry");
+    static_assert(PITCH % 64 == 0, "stem geometry");
 };
 
-template <int CC, int R, int S, int F, int PITCH>
+template <int CC, int R, int S, int F, int PITCH, int ST>
 __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
+    static_assert((16 * F - 1) * ST + S <= PITCH, "every lane's taps inside its halo row");
     using Geo = StemGeo<CC, R, S, PITCH>;
-    constexpr int SP = Geo::SP;
-    constexpr int NK = CC * R * 2;  // k-steps of a row
+    constexpr int CRS = Geo::CRS;
+    constexpr int NK = Geo::WK / 4;  // k-steps of a row
     constexpr int LPR = PITCH / 64;
 
     extern __shared__ float smem[];
@@ -79,18 +80,16 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
         buf_rsrc(a.x + (int64_t)n * a.x_img, (uint32_t)(a.x_img * 4));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, a.w_bytes);
 
-    // The filter: row o of the LDS copy holds w[co0 + o][c][r][s] at
-    // (c*R + r)*8 + s, zeros for s >= S and for channels past K.
+    // The filter: row o of the LDS copy holds w[co0 + o] as stored, k =
+    // (c*R + r)*S + s, zeros for k >= C*R*S and for channels past K.
     {
         constexpr int NI = Geo::WS / 64;
         for (int i = wv; i < NI; i += 8) {
             const int e = i * 64 + lane;
             const int row = e / Geo::WP, col = e - (e / Geo::WP) * Geo::WP;
-            const int c = col / (R * SP), rs = col - c * (R * SP);
-            const int r = rs / SP, s = rs - r * SP;
             const int co = co0 + row;
-            const bool ok = row < 64 && co < a.K && col < Geo::WK && s < S;
-            lds_dma_b32(rw, ws + i * 64, ok ? (((co * CC + c) * R + r) * S + s) * 4 : kOOB);
+            const bool ok = row < 64 && co < a.K && col < CRS;
+            lds_dma_b32(rw, ws + i * 64, ok ? (co * CRS + col) * 4 : kOOB);
         }
     }
     // Halo of output row oy: channel c, row r, column col at c*CP + r*PITCH +
@@ -122,13 +121,21 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
             }
     };
 
-    // Per-lane bases: B, the lane's pixel column plus its tap lg; A, the
-    // lane's output channel row plus lg.
-    int pix[F];
+    // Per-lane bases.  k-step t takes k = 4t + lg: B reads the halo at the
+    // lane's pixel column plus the tap's offset toff[t] (per lane: the four
+    // lane groups' taps straddle filter rows); the padding k >= C*R*S reads
+    // tap 0, times a zero weight.  A reads the lane's output channel row at
+    // 4t + lg.
+    // Fragment f adds the constant 16 f ST; lanes past the row's end read
+    // inside the halo row (the pitch holds all 16 F columns) and are not
+    // stored.
+    const int pix0 = l16 * ST;
+    int toff[NK];
 #pragma unroll
-    for (int f = 0; f < F; ++f) {
-        const int ox = min(f * 16 + l16, a.OW - 1);
-        pix[f] = ox * a.st + lg;
+    for (int t = 0; t < NK; ++t) {
+        const int k = 4 * t + lg;
+        const int c = k / (R * S), rs = k - c * (R * S), r = rs / S, sx = rs - r * S;
+        toff[t] = k < CRS ? c * Geo::CP + r * PITCH + sx : 0;
     }
     const int abase = (wq * 16 + l16) * Geo::WP + lg;
 
@@ -138,11 +145,10 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
 
     auto fetch = [&](const float *hs, const int kk, float (&bv)[F], float &av)
         __attribute__((always_inline)) {
-        const int c = kk / (2 * R), r = (kk / 2) % R, h = kk % 2;
-        av = ws[abase + (c * R + r) * SP + 4 * h];
-        const int toff = c * Geo::CP + r * PITCH + 4 * h;
+        av = ws[abase + 4 * kk];
+        const float *hb = hs + pix0 + toff[kk];
 #pragma unroll
-        for (int f = 0; f < F; ++f) bv[f] = hs[pix[f] + toff];
+        for (int f = 0; f < F; ++f) bv[f] = hb[16 * f * ST];
     };
     auto mma = [&](const float (&bv)[F], const float av) __attribute__((always_inline)) {
 #pragma unroll
@@ -166,8 +172,8 @@ __global__ void __launch_bounds__(512, 1) stem_fwd_kernel(const StemArgs a) {
     };
     // Fragment f, register v: output channel 4*lg + v of the wave's 16,
     // pixel 16f + l16 of the row.  A non-finite sum may hold a product the
-    // reference skips (the zero weight of tap s = 7 times real x, or a weight
-    // times the halo's padding): the lane notes it, and after the last row
+    // reference skips (the zero weight of a padding k times real x, or a
+    // weight times the halo's padding): the lane notes it, and after the last row
     // re-reads its own outputs and recomputes the non-finite ones over the
     // visited products (exact.hpp), keeping that code out of the row loop.
     float *ybase = a.y + (int64_t)n * a.y_img;

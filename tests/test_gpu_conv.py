@@ -242,6 +242,29 @@ def test_stem_forward_direct(xs, dev):
     assert_within(y.cpu().numpy(), y_ref, ys, xs[1] * 49, f"stem fwd {xs}")
 
 
+@pytest.mark.parametrize("xs,k,st", [((2, 3, 224, 224), 64, 2),   # the stem at batch 2
+                                     ((3, 3, 129, 130), 70, 2),   # 65-pixel rows; 70 outputs
+                                     ((2, 3, 100, 111), 64, 1),   # stride 1: 111-pixel rows
+                                     ((1, 3, 40, 64), 16, 1)])    # 64-pixel rows, 16 outputs
+def test_stem_forward(xs, k, st, dev):
+    """Forward of 3-channel 7x7 layers with padding 3 (the stem kernel:
+    k = (c, r, s) in the filter's order, 37 k-steps, each lane's tap offset
+    in a register) against the oracle: rows shorter than the 112 pixels the
+    waves cover (the lanes past the end are computed and not stored), an
+    output-channel block of 6, both strides."""
+    import torch
+
+    from katsu_amd import ops
+    ws = (k, 3, 7, 7)
+    x = synth.uniform(341, xs)
+    w = synth.normal(342, ws)
+    y = ops.conv2d_forward(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), st, 3)
+    torch.cuda.synchronize()
+    ref = O.conv2d_forward(x, w, st, 3)
+    sab = O.conv2d_forward(np.abs(x), np.abs(w), st, 3)
+    assert_within(y.cpu().numpy(), ref, sab, 147, f"stem fwd {xs} k{k} s{st}")
+
+
 @pytest.mark.parametrize("xs", [(4, 3, 224, 224), (5, 3, 61, 150), (1, 3, 20, 300)])
 def test_stem_filter_gradient(xs, dev):
     """7x7 stride-2 filter gradient of a 3-channel layer (the stem kernel:
