@@ -425,9 +425,12 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
                         const int i = i0 + wi0 + FM * (4 * lg + v) + a;
                         if (i >= g.M) continue;
                         float *blk = col + (int64_t)i * g.HW;
-                        *reinterpret_cast<floatx4 *>(blk) =
-                            floatx4{acc[a][0][v], 0.f, acc[a][1][v], 0.f};
-                        *reinterpret_cast<floatx4 *>(blk + g.W) = floatx4{0.f, 0.f, 0.f, 0.f};
+                        // Streamed past the caches: nothing in this launch
+                        // reads dx back.
+                        __builtin_nontemporal_store(floatx4{acc[a][0][v], 0.f, acc[a][1][v], 0.f},
+                                                    reinterpret_cast<floatx4 *>(blk));
+                        __builtin_nontemporal_store(floatx4{0.f, 0.f, 0.f, 0.f},
+                                                    reinterpret_cast<floatx4 *>(blk + g.W));
                     }
             }
             return;
