@@ -52,13 +52,6 @@ struct PwGeo {
     static constexpr size_t kBytes = 2 * (size_t)STAGE * sizeof(float);
 };
 
-// Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
-// passes of pw_bwd_kernel).
-// V: 0 scalar loads; bit 0 the A operand 16 bytes at a time (the weight in
-// MODE 0 and 1: C % 4 = 0, w 16-byte aligned; G along four adjacent pixels
-// in MODE 2: OH*OW % 4 = 0, G 16-byte aligned); V = 3 also G 16 bytes at a
-// time in MODE 1 (same condition), each thread then taking four adjacent
-// pixel columns.
 // A value the compiler may not reason about: a buffer offset selected
 // between an address and kOOB stays one unconditional load, instead of
 // being split into a branch around the load.
@@ -67,6 +60,13 @@ __device__ __forceinline__ int vopaque(int v) {
     return v;
 }
 
+// Block `bid` of the `nb` blocks of pass g (pw_kernel, or one of the two
+// passes of pw_bwd_kernel).
+// V: 0 scalar loads; bit 0 the A operand 16 bytes at a time (the weight in
+// MODE 0 and 1: C % 4 = 0, w 16-byte aligned; G along four adjacent pixels
+// in MODE 2: OH*OW % 4 = 0, G 16-byte aligned); V = 3 also G 16 bytes at a
+// time in MODE 1 (same condition), each thread then taking four adjacent
+// pixel columns.
 template <int MODE, int BM, int V, int PF = 1>
 __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
     constexpr bool AV = (V & 1) != 0, BV = MODE == 1 && (V & 2) != 0;
@@ -303,7 +303,8 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
 #pragma unroll
                     for (int q = 0; q < NB / 4; ++q) {
                         const int k = k0 + q * 16 + (tid >> 4);
-                        const int off = vopaque((colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
+                        const int off = vopaque(
+                            (colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
                         const floatx4 v = __builtin_bit_cast(
                             floatx4, __builtin_amdgcn_raw_buffer_load_b128(rgg, off, 0, 0));
 #pragma unroll
@@ -313,7 +314,8 @@ __device__ __forceinline__ void pw_block(const PwArgs &g, int bid, int nb) {
 #pragma unroll
                     for (int q = 0; q < NB; ++q) {
                         const int k = k0 + q * 4 + (tid >> 6);
-                        const int off = vopaque((colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
+                        const int off = vopaque(
+                            (colok && k < ke) ? (int)(colg + (int64_t)k * g.OHW) * 4 : kOOB);
                         xb[q] = __builtin_bit_cast(
                             float, __builtin_amdgcn_raw_buffer_load_b32(rgg, off, 0, 0));
                     }
