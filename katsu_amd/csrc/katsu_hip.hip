@@ -363,7 +363,7 @@ bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, i
 #define KATSU_GEMM_RD 1
 #endif
 #ifndef KATSU_GEMM_RD_D
-#define KATSU_GEMM_RD_D 4
+#define KATSU_GEMM_RD_D 3
 #endif
 #ifndef KATSU_GEMM_RD_VJP_D
 #define KATSU_GEMM_RD_VJP_D 3
@@ -373,6 +373,9 @@ bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, i
 #endif
 #ifndef KATSU_GEMM_RD_VJP_KS
 #define KATSU_GEMM_RD_VJP_KS 4
+#endif
+#ifndef KATSU_GEMM_RD_VJP_OCC
+#define KATSU_GEMM_RD_VJP_OCC 1  // blocks per CU the VJP kernel is built for
 #endif
 // K = 1024: KS waves of 1024 / KS each, in blocks of 16.
 constexpr int kRdK = 1024;
@@ -525,7 +528,7 @@ int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, fl
             rb.c = db;
             const int nb0 = ra.tiles_m * ra.tiles_n, nb1 = rb.tiles_m * rb.tiles_n;
             constexpr auto kern =
-                gemm_rd_vjp_kernel<kRdVjpKs, kRdVjpNkb, KATSU_GEMM_RD_VJP_D, 8 / kRdVjpKs>;
+                gemm_rd_vjp_kernel<kRdVjpKs, kRdVjpNkb, KATSU_GEMM_RD_VJP_D, KATSU_GEMM_RD_VJP_OCC>;
             constexpr size_t lds = kRdVjpKs * 64 * 64 * 4;
             const int rc = lds_optin<kern>(lds);
             if (rc != KATSU_OK) return rc;
