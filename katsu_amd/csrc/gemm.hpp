@@ -29,6 +29,7 @@ struct GemmArgs {
     int tiles_m, tiles_n, splits, kchunk;  // kchunk: k range of one split (multiple of 16)
     int64_t split_stride;                  // floats between partial slices, or 0
     uint32_t a_bytes, b_bytes;
+    int gm;  // register-direct GEMM: tile rows per group of consecutive tiles (divides tiles_m)
 };
 
 template <int BM, int BN, int BK_, bool TA, bool TB>
@@ -336,7 +337,11 @@ __device__ __forceinline__ void gemm_rd_block(const GemmArgs &g, int bid, int nb
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g4 = lane >> 4;
     const int tile = xcd_swizzle(bid, nb);
-    const int i0 = (tile % g.tiles_m) * T, j0 = (tile / g.tiles_m) * T;
+    // Tiles in groups of gm tile rows, row fastest within a group: the
+    // consecutive tiles one XCD takes cover a patch gm rows tall, so its L2
+    // holds fewer operand panels (gm = tiles_m is plain column order).
+    const int gsz = g.gm * g.tiles_n, grp = tile / gsz, gi = tile - grp * gsz;
+    const int i0 = (grp * g.gm + gi % g.gm) * T, j0 = (gi / g.gm) * T;
     const int kb0 = w * NKB * 16;  // K = KS * NKB * 16 (host-checked)
 
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(g.a, g.a_bytes);

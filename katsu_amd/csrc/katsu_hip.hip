@@ -404,6 +404,9 @@ bool gemm_rd_plan(const float *a, const float *b, const float *c, int64_t M, int
     g->beta = beta;
     g->tiles_m = (int)(M / 64);
     g->tiles_n = (int)(N / 64);
+    // Groups of four tile rows per patch (1024^2: each XCD's 32 tiles read
+    // 4 row and 8 column panels, 3 MB), else plain column order.
+    g->gm = g->tiles_m % 4 == 0 ? 4 : g->tiles_m;
     g->splits = 1;
     g->kchunk = 0;  // set by the kernel's KS
     g->a_bytes = (uint32_t)(M * K * 4);

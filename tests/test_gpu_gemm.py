@@ -64,10 +64,11 @@ def test_matmul_and_vjp_parity(m, k, n, dev):
 # (m, n, k): unaligned (the generic engine), then multiples of 4 (the
 # dedicated GEMM: 64-tiles with split-K, a long split-K reduction, 128-tiles
 # with edge tiles, 32-tiles at 512 deep), then the register-direct GEMM
-# (64-tiles, K = 1024 in four wave quarters).
+# (64-tiles, K = 1024 in four wave quarters; tiles in patches of four tile
+# rows, or in column order when the tile rows are not a multiple of four).
 @pytest.mark.parametrize("m,n,k", [(70, 45, 131), (72, 44, 132), (128, 96, 2048),
                                    (516, 260, 68), (1024, 512, 1024), (512, 512, 512),
-                                   (256, 640, 512)])
+                                   (256, 640, 512), (192, 2752, 1024)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_all_transposes_beta(ta, tb, m, n, k, dev):
     import torch
