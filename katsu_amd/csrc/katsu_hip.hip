@@ -301,6 +301,9 @@ int gemm_fast_wg(const GemmArgs &g, int64_t blocks, int wg, int ta, int tb, hipS
 #endif
 
 // The dedicated GEMM (gemm.hpp) for aligned problems: the tile, the split of
+#ifndef KATSU_GEMM_BK32
+#define KATSU_GEMM_BK32 64  // k-tile depth of the 32 x 32 GEMM tiles
+#endif
 // K and the launch arguments (C not bound yet).  False = not applicable.
 struct GemmFastPlan {
     GemmArgs g{};
@@ -330,7 +333,7 @@ bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, i
         splits = std::max<int64_t>(
             1, std::min<int64_t>(cdiv(KATSU_GEMM_TARGET, tiles), K / KATSU_GEMM_KMIN64));
     }
-    const int64_t kq = T == 128 ? 16 : T == 64 ? KATSU_GEMM_BK64 : 32;  // the tile's k depth
+    const int64_t kq = T == 128 ? 16 : T == 64 ? KATSU_GEMM_BK64 : KATSU_GEMM_BK32;  // k depth
     const int64_t kchunk = (cdiv(K, splits) + kq - 1) / kq * kq;
     splits = cdiv(K, kchunk);
     GemmArgs &g = pl->g;
@@ -452,7 +455,7 @@ bool gemm_fast(const float *a, const float *b, float *c, int64_t M, int64_t N, i
     const int wg = pl.blocks < KATSU_GEMM_WG2_BELOW ? 2 : 1;
     *rc = pl.T == 128  ? gemm_fast_wg<128, 128, 16>(g, pl.blocks, wg, ta, tb, st)
           : pl.T == 64 ? gemm_fast_wg<64, 64, KATSU_GEMM_BK64>(g, pl.blocks, wg, ta, tb, st)
-                       : gemm_fast_wg<32, 32, 32>(g, pl.blocks, wg, ta, tb, st);
+                       : gemm_fast_wg<32, 32, KATSU_GEMM_BK32>(g, pl.blocks, wg, ta, tb, st);
     if (*rc == KATSU_OK && pl.splits > 1)
         *rc = launch_split_reduce(ws, c, M * N, pl.pstride, (int)pl.splits, beta, st);
     return true;
@@ -558,8 +561,8 @@ int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, fl
             if (pa.T == 64)
                 return two ? gemm_vjp_launch<64, 64, KATSU_GEMM_BK64, 2>(pa.g, pb.g, b0, b1, st)
                            : gemm_vjp_launch<64, 64, KATSU_GEMM_BK64, 1>(pa.g, pb.g, b0, b1, st);
-            return two ? gemm_vjp_launch<32, 32, 32, 2>(pa.g, pb.g, b0, b1, st)
-                       : gemm_vjp_launch<32, 32, 32, 1>(pa.g, pb.g, b0, b1, st);
+            return two ? gemm_vjp_launch<32, 32, KATSU_GEMM_BK32, 2>(pa.g, pb.g, b0, b1, st)
+                       : gemm_vjp_launch<32, 32, KATSU_GEMM_BK32, 1>(pa.g, pb.g, b0, b1, st);
         }
     }
     int rc = KATSU_OK;
