@@ -53,6 +53,43 @@ def test_conv_step_graph_replays(name, batch, dev):
             assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("name,batch", [("c4b_down1x1", 32), ("c5_stem", 2)])
+def test_one_call_backward_graph_replays(name, batch, dev):
+    """The forward and the one-call backward of the 1x1 layer at full size
+    (register-direct forward; dX and dW in one launch with two k-tiles of
+    buffer loads in flight, non-temporal dX stores; the dW reduce) and of the
+    stem (flat-reduction forward; rolling-row dX, dW and reduce)."""
+    import torch
+
+    from katsu_amd import ops
+    c = dict(synth.CONV_CONFIGS[name])
+    c["x"] = (batch,) + c["x"][1:]
+    x, w = synth.conv_inputs(c)
+    st, p = c["stride"], c["pad"]
+    g = synth.normal(synth.SEED_G, synth.out_shape(c))
+    xd, wd, gd = (torch.from_numpy(a).to(dev) for a in (x, w, g))
+    y = torch.empty(synth.out_shape(c), device=dev)
+    dx = torch.empty_like(xd)
+    dw = torch.empty_like(wd)
+
+    def step():
+        ops.conv2d_forward(xd, wd, st, p, out=y)
+        ops.conv2d_backward(xd, wd, gd, st, p, dx=dx, dw=dw)
+
+    step()
+    torch.cuda.synchronize()
+    ref = (y.clone(), dx.clone(), dw.clone())
+    graph = _capture(step)
+    for _ in range(3):
+        for t in (y, dx, dw):
+            t.fill_(float("nan"))  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((y, dx, dw), ref):
+            assert torch.equal(got, want)
+
+
 def test_matmul_vjp_graph_replays(dev):
     import torch
 
