@@ -1170,7 +1170,7 @@ __device__ __forceinline__ void direct_dw_block(const DirectDwArgs &a, int bid, 
                 floatx4 v = *reinterpret_cast<const floatx4 *>(src + c4 * 4);
                 floatx4 *d = reinterpret_cast<floatx4 *>(dst + c4 * 4);
                 if (a.split_stride == 0 && a.beta != 0.f) v += *d;
-                *d = v;
+                __builtin_nontemporal_store(v, d);  // read back by the next kernel only
             }
         } else {
             for (int e = lane; e < len; e += 64) {

@@ -241,9 +241,9 @@ __device__ __forceinline__ void store_beta(float *p, float v, float beta) {
 // The same for the direct convolution kernels' output stream (written once,
 // read by a later kernel): a non-temporal store, which drained faster at the
 // end of a block there (config 3: forward and dX about 1 us faster), as do
-// the 1x1 dX's whole 2 x 4 blocks (pointwise.hpp).  It is slower for
-// scattered single floats and for the GEMM's tiles, which keep ordinary
-// stores.
+// the 1x1 dX's whole 2 x 4 blocks (pointwise.hpp) and the direct dW's
+// 16-byte partial runs.  It is slower for scattered single floats and for
+// the GEMM's tiles, which keep ordinary stores.
 __device__ __forceinline__ void store_beta_nt(float *p, float v, float beta) {
     __builtin_nontemporal_store((beta == 0.f) ? v : beta * *p + v, p);
 }
