@@ -155,14 +155,51 @@ def test_filter_gradient_is_deterministic(dev):
 @pytest.mark.parametrize("name,batch", [("c1_example", 1), ("c3_resnet", 2),
                                         ("c4a_down3x3", 2), ("c4b_down1x1", 2),
                                         ("c5_stem", 1)])
-def test_baseline_configs_reduced_batch(name, batch, dev):
-    """The BASELINE layer shapes at a reduced batch, full oracle comparison
-    with a random upstream gradient (all-ones would hide a flipped kernel)."""
+def test_baseline_layers_small_batch(name, batch, dev):
+    """The BASELINE layers' channel and kernel shapes at a batch of 1 or 2,
+    full oracle comparison with a random upstream gradient (all-ones would
+    hide a flipped kernel).  At these batches configs 3 and 4a take the
+    generic engine (too few tiles for the direct kernels); the production
+    kernels are the next test's."""
     c = dict(synth.CONV_CONFIGS[name])
     c["x"] = (batch,) + c["x"][1:]
     x, w = synth.conv_inputs(c)
     g = synth.normal(synth.SEED_G, synth.out_shape(c))
     _check_full(x, w, g, c["stride"], c["pad"], dev, name)
+
+
+@pytest.mark.parametrize("name,batch", [("c3_resnet", 9), ("c4a_down3x3", 16),
+                                        ("c5_stem", 9), ("c4b_down1x1", 32)])
+def test_production_kernels_full_parity(name, batch, dev):
+    """The kernels the BASELINE configurations run (the direct 3x3 kernels of
+    configs 3 and 4a and their one-launch backward, the stem's kernels, the
+    1x1 kernels) at the smallest batch where the planner picks them: every
+    element of y, dX and dW, from the separate calls and from the one-call
+    backward, against the oracle on finite random data."""
+    import torch
+
+    from katsu_amd import ops
+    c = dict(synth.CONV_CONFIGS[name])
+    c["x"] = (batch,) + c["x"][1:]
+    x, w = synth.conv_inputs(c)
+    g = synth.normal(synth.SEED_G, synth.out_shape(c))
+    st, p = c["stride"], c["pad"]
+    print(f"\n{name} N={batch}", flush=True)
+    y, dx, dw = _run(x, w, g, st, p, dev)
+    xd, wd, gd = (torch.from_numpy(a).to(dev) for a in (x, w, g))
+    dx1, dw1 = ops.conv2d_backward(xd, wd, gd, st, p)
+    torch.cuda.synchronize()
+    k, ci, r, s = w.shape
+    n, _, oh, ow = g.shape
+    y_ref = O.conv2d_forward(x, w, st, p)
+    dx_ref, dw_ref = O.conv2d_backward(x, w, g, st, p)
+    ys = O.conv2d_forward(np.abs(x), np.abs(w), st, p)
+    dxs, dws = O.conv2d_backward(np.abs(x), np.abs(w), np.abs(g), st, p)
+    assert_within(y, y_ref, ys, ci * r * s, f"{name} fwd")
+    for what, got_dx, got_dw in (("separate", dx, dw),
+                                 ("one-call", dx1.cpu().numpy(), dw1.cpu().numpy())):
+        assert_within(got_dx, dx_ref, dxs, k * r * s, f"{name} {what} dX")
+        assert_within(got_dw, dw_ref, dws, n * oh * ow, f"{name} {what} dW")
 
 
 def test_repo_example_config1(dev):
