@@ -190,6 +190,12 @@ int katsu_hip_conv2d_bwd_f32_dev_noalloc(const float *x, const float *w, const f
                                          float beta, void *stream);
 size_t katsu_hip_noalloc_scratch_bytes(void);
 
+/* Number of device allocations (hipMalloc) this library has made since it
+ * was loaded: its scratch and staging buffers and the katsu_hip_malloc pool.
+ * No counterpart in the reference; it lets a caller that cannot allocate
+ * check that a code path allocated nothing (the count does not change). */
+uint64_t katsu_hip_device_allocations(void);
+
 /* ---- Device residency and the engine's elementwise work -----------------
  * For callers that keep tensor data on the GPU between calls (a device
  * mirror per immutable node, tensor.rs:96-107), accumulate adjoints in
@@ -254,7 +260,10 @@ int katsu_hip_gradcam_f32_dev(const float *act, const float *grad, size_t n, siz
  * centres.  Output row oy samples source row
  * sy = max(0, (oy + 0.5) * ih/oh - 0.5) and blends rows floor(sy) and
  * floor(sy) + 1 (clamped to ih - 1) with weights 1 - f and f,
- * f = sy - floor(sy); columns likewise.  Equal sizes copy exactly.
+ * f = sy - floor(sy); columns likewise.  Each blend is rounded as
+ * (1 - f)*a + f*b (no fused multiply-add); a neighbour of weight exactly 0 is
+ * left out, so NaN or Inf reaches only the outputs that use that pixel.
+ * Equal sizes copy every value as it is, non-finite ones included.
  * ih*iw and oh*ow must each be <= 2^31 - 1.  No counterpart in the
  * reference's code. */
 int katsu_hip_resize_bilinear_f32_dev(const float *src, size_t n, size_t ih, size_t iw,

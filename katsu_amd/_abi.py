@@ -22,6 +22,7 @@ EXPORTS = (
     "katsu_hip_conv2d_bwd_filter_f32", "katsu_hip_conv2d_bwd_filter_f32_dev",
     "katsu_hip_conv2d_bwd_f32", "katsu_hip_conv2d_bwd_f32_dev",
     "katsu_hip_conv2d_bwd_f32_dev_noalloc", "katsu_hip_noalloc_scratch_bytes",
+    "katsu_hip_device_allocations",
     "katsu_hip_stream", "katsu_hip_malloc", "katsu_hip_free", "katsu_hip_upload",
     "katsu_hip_download", "katsu_hip_sync",
     "katsu_hip_add_f32_dev", "katsu_hip_mul_f32_dev", "katsu_hip_accumulate_f32_dev",
@@ -97,9 +98,12 @@ def lib():
         L.katsu_hip_resize_bilinear_f32_dev.argtypes = [vp, sz, sz, sz, sz, sz, vp, vp]
         for name in EXPORTS:
             if name not in ("katsu_hip_version", "katsu_hip_strerror", "katsu_hip_shutdown",
-                            "katsu_hip_noalloc_scratch_bytes"):
+                            "katsu_hip_noalloc_scratch_bytes",
+                            "katsu_hip_device_allocations"):
                 getattr(L, name).restype = i
         L.katsu_hip_noalloc_scratch_bytes.restype = sz
+        L.katsu_hip_device_allocations.argtypes = []
+        L.katsu_hip_device_allocations.restype = ctypes.c_uint64
         _lib = L
     return _lib
 

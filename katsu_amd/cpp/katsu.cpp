@@ -123,20 +123,17 @@ Result<DeviceBuf> device_buffer(size_t count) {
     return b;
 }
 
-// A zero-filled device buffer (zeros_buffer, tensor.rs:120-125, on the GPU).
-Result<DeviceBuf> device_zeros(size_t count) {
-    KATSU_TRY(b, device_buffer(count));
-    const int rc = katsu_hip_fill_f32_dev(b.get(), count, 0.0f, stream());
-    if (rc != KATSU_OK) return device(rc);
-    return b;
-}
 
 bool checked_mul(size_t a, size_t b, size_t *out) { return !__builtin_mul_overflow(a, b, out); }
 bool checked_add(size_t a, size_t b, size_t *out) { return !__builtin_add_overflow(a, b, out); }
 
 }  // namespace
 
+// The fault-injection hook of the all-or-nothing publication test exists
+// only in test builds (KATSU_TESTING); elsewhere publication never fails on
+// purpose.
 namespace testing {
+#ifdef KATSU_TESTING
 static std::atomic<int> publish_countdown{-1};
 void fail_publish_after(int n) { publish_countdown.store(n); }
 // True once the countdown set by fail_publish_after reaches zero.
@@ -148,6 +145,9 @@ static bool publish_fault() {
     }
     return false;
 }
+#else
+static constexpr bool publish_fault() { return false; }
+#endif
 }  // namespace testing
 
 // tensor.rs:32-67.

@@ -229,13 +229,16 @@ Result<size_t> element_count(const std::vector<size_t> &shape);
 Result<Tensor> mean_pool_hw(const Tensor &y);
 Result<Tensor> spread_hw(const Tensor &dp, const std::vector<size_t> &shape);
 
+#ifdef KATSU_TESTING
 namespace testing {
 // Test support for the all-or-nothing publication of backward_with
-// (tensor.rs:341-360): the engine's publication step reports a failed device
-// call (TensorError::Device) after n more successful accumulation launches;
-// n < 0 (the default) never.  Forces the condition from the host, so no
-// kernel misbehaves.
+// (tensor.rs:341-360), compiled only into test builds (KATSU_TESTING): the
+// engine's publication step reports a failed device call
+// (TensorError::Device) after n more successful accumulation launches; n < 0
+// (the default) never.  Forces the condition from the host, so no kernel
+// misbehaves.
 void fail_publish_after(int n);
 }  // namespace testing
+#endif
 
 }  // namespace katsu

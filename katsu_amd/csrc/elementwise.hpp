@@ -272,14 +272,30 @@ __global__ void __launch_bounds__(256) normalize_rows_by_max(float *x, int64_t c
 // half-pixel centres.  Output row oy samples source row
 // sy = max(0, (oy + 0.5) * IH/OH - 0.5); it blends rows floor(sy) and
 // floor(sy) + 1 (clamped to the last row) with weights 1 - f and f,
-// f = sy - floor(sy); columns likewise.  Same size is an exact copy.
+// f = sy - floor(sy); columns likewise.  Each blend is rounded as written,
+// (1 - f) * a + f * b with no fused multiply-add, and a neighbour whose
+// weight is exactly 0 is left out (so a non-finite pixel reaches only the
+// outputs that use it).  Equal sizes copy every pixel as it is.
+__device__ __forceinline__ float blend_lin(float a, float b, float f) {
+#pragma clang fp contract(off)
+    if (f == 0.f) return a;
+    if (f == 1.f) return b;
+    return (1.f - f) * a + f * b;
+}
+
 __global__ void __launch_bounds__(256) resize_bilinear(const float *__restrict__ src, int64_t N,
                                                        int IH, int IW, int OH, int OW,
                                                        float *__restrict__ dst) {
+#pragma clang fp contract(off)
     const int64_t ohw = (int64_t)OH * OW, total = N * ohw;
+    const bool same = IH == OH && IW == OW;
     const float sh = (float)IH / (float)OH, sw = (float)IW / (float)OW;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        if (same) {
+            dst[i] = src[i];
+            continue;
+        }
         const int64_t n = i / ohw;
         const int p = (int)(i - n * ohw), oy = p / OW, ox = p - (p / OW) * OW;
         const float sy = fmaxf(((float)oy + 0.5f) * sh - 0.5f, 0.f);
@@ -288,9 +304,9 @@ __global__ void __launch_bounds__(256) resize_bilinear(const float *__restrict__
         const int y1 = min(y0 + 1, IH - 1), x1 = min(x0 + 1, IW - 1);
         const float fy = fminf(sy - (float)y0, 1.f), fx = fminf(sx - (float)x0, 1.f);
         const float *s = src + n * IH * IW;
-        const float top = (1.f - fx) * s[y0 * IW + x0] + fx * s[y0 * IW + x1];
-        const float bot = (1.f - fx) * s[y1 * IW + x0] + fx * s[y1 * IW + x1];
-        dst[i] = (1.f - fy) * top + fy * bot;
+        const float top = blend_lin(s[y0 * IW + x0], s[y0 * IW + x1], fx);
+        const float bot = blend_lin(s[y1 * IW + x0], s[y1 * IW + x1], fx);
+        dst[i] = blend_lin(top, bot, fy);
     }
 }
 

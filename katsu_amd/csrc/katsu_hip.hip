@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -71,6 +72,11 @@ State &state() {
     return s;
 }
 
+// Device allocations this library has made (every successful hipMalloc of
+// the scratch buffers, the staging buffers and the caller pool), for callers
+// that check that a code path allocates nothing.
+std::atomic<uint64_t> g_device_allocs{0};
+
 int map_hip(hipError_t e) {
     if (e == hipSuccess) return KATSU_OK;
     if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return KATSU_E_OOM;
@@ -113,6 +119,7 @@ int scratch_get(ScratchKind kind, hipStream_t, size_t bytes, float **out) {
             (void)hipGetLastError();
             return map_hip(e);
         }
+        g_device_allocs.fetch_add(1, std::memory_order_relaxed);
         if (b.ptr) p.retired.push_back(b.ptr);
         b.ptr = ptr;
         b.bytes = want;
@@ -181,6 +188,7 @@ int ensure(Buffer &b, size_t bytes) {
         b.ptr = nullptr;
         return map_hip(e);
     }
+    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
     b.bytes = want;
     return KATSU_OK;
 }
@@ -2395,6 +2403,7 @@ int pool_alloc(State &s, size_t bytes, void **out) {
         e = hipMalloc(&p, want);
         if (e != hipSuccess) return map_hip(e);
     }
+    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
     s.pool.live.emplace(p, want);
     *out = p;
     return KATSU_OK;
@@ -2631,6 +2640,10 @@ int katsu_hip_conv2d_bwd_f32_dev_noalloc(const float *x, const float *w, const f
 }
 
 size_t katsu_hip_noalloc_scratch_bytes(void) { return kStaticScratchBytes; }
+
+uint64_t katsu_hip_device_allocations(void) {
+    return g_device_allocs.load(std::memory_order_relaxed);
+}
 
 int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, float *dx,
                              float *dw, const katsu_conv_geom *g, float beta) {

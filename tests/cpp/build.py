@@ -1,5 +1,8 @@
 """Builds the C++ front-end test driver tests/cpp/_build/test_frontend
-(test infrastructure; links katsu_amd/lib/libkatsu.so)."""
+(test infrastructure).  The front end (katsu_amd/cpp/katsu.cpp) is compiled
+into the driver with KATSU_TESTING, which adds the publication fault hook
+that the production libkatsu.so leaves out; the kernels come from
+katsu_amd/lib/libkatsu_hip.so."""
 import os
 import subprocess
 import sys
@@ -14,8 +17,10 @@ def build(verbose: bool = False) -> str:
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
     tmp = OUT + ".tmp"
     rpath = "-Wl,-rpath,$ORIGIN/../../../katsu_amd/lib"
-    cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", os.path.join(HERE, "test_frontend.cpp"),
-           "-o", tmp, "-L", LIB_DIR, "-lkatsu", "-lkatsu_hip", rpath]
+    cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-DKATSU_TESTING",
+           os.path.join(HERE, "test_frontend.cpp"),
+           os.path.join(ROOT, "katsu_amd", "cpp", "katsu.cpp"),
+           "-o", tmp, "-L", LIB_DIR, "-lkatsu_hip", rpath]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

@@ -176,3 +176,17 @@ def test_overlapping_backward_outputs_are_rejected():
     # The same buffer with different sizes cannot be one node's pending buffer.
     g2 = katsu_amd.geometry(2, 3, 5, 5, 4, 3, 3, 1, 1)
     assert L.katsu_hip_conv2d_bwd_f32(x, x, x, dx, dx, ctypes.byref(g2), 1.0) == _abi.E_INVALID
+
+
+def test_noalloc_scratch_covers_every_plan():
+    """Every BASELINE layer's dW workspace fits the static scratch of the
+    allocation-free backward (host-side plans only; no GPU)."""
+    from katsu_amd import synth
+    lim = _abi.lib().katsu_hip_noalloc_scratch_bytes()
+    assert lim == 40 << 20
+    for name, c in synth.CONV_CONFIGS.items():
+        g = katsu_amd.geometry(*c["x"], c["w"][0], c["w"][2], c["w"][3], c["stride"], c["pad"])
+        need = ctypes.c_size_t(0)
+        assert _abi.lib().katsu_hip_conv2d_bwd_filter_workspace(ctypes.byref(g),
+                                                                  ctypes.byref(need)) == 0
+        assert 0 <= need.value <= lim, (name, need.value)

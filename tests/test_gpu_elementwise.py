@@ -135,8 +135,55 @@ def test_resize_bilinear(dev, src, dst):
                         mode="bilinear", align_corners=False)[:, 0].numpy()
     assert got.shape == (n, *dst)
     assert np.max(np.abs(got - ref)) <= 2e-7
+    assert np.array_equal(got, _resize_f32(maps, dst))
     if src == dst:
         assert np.array_equal(got, maps)
+
+
+def _resize_f32(maps, size):
+    """The kernel's formula evaluated in float32 by numpy, rounding as written:
+    per blend (1 - f)*a + f*b, a weight of exactly 0 leaving its neighbour
+    out; equal sizes copy."""
+    n, ih, iw = maps.shape
+    oh, ow = size
+    if (ih, iw) == (oh, ow):
+        return maps.copy()
+    f32 = np.float32
+
+    def axis(o, i):
+        s = np.maximum((np.arange(o, dtype=f32) + f32(0.5)) * (f32(i) / f32(o)) - f32(0.5), f32(0))
+        lo = np.minimum(s.astype(np.int64), i - 1)
+        hi = np.minimum(lo + 1, i - 1)
+        return lo, hi, np.minimum(s - lo.astype(f32), f32(1))
+
+    def blend(a, b, f):
+        with np.errstate(invalid="ignore", over="ignore"):
+            mix = (f32(1) - f) * a + f * b
+        return np.where(f == 0, a, np.where(f == 1, b, mix)).astype(f32)
+
+    y0, y1, fy = axis(oh, ih)
+    x0, x1, fx = axis(ow, iw)
+    top = blend(maps[:, y0][:, :, x0], maps[:, y0][:, :, x1], fx[None, None, :])
+    bot = blend(maps[:, y1][:, :, x0], maps[:, y1][:, :, x1], fx[None, None, :])
+    return blend(top, bot, fy[None, :, None])
+
+
+@pytest.mark.parametrize("src,dst", [((7, 9), (14, 18)), ((7, 9), (7, 9)), ((5, 6), (11, 4))])
+def test_resize_bilinear_nonfinite(dev, src, dst):
+    """Inf and NaN pixels: an equal-size resize copies them; otherwise they
+    reach only the outputs whose blend gives them a non-zero weight (the
+    float32 formula's masks and values, exactly)."""
+    import torch
+
+    from katsu_amd import ops
+    maps = np.abs(synth.uniform(22, (2, *src)))
+    maps[0, 0, 0] = np.inf
+    maps[1, src[0] // 2, src[1] - 1] = np.nan
+    maps[1, src[0] - 1, 1] = -np.inf
+    got = ops.resize_bilinear(torch.from_numpy(maps).to(dev), dst).cpu().numpy()
+    ref = _resize_f32(maps, dst)
+    assert np.isfinite(ref).any() and not np.isfinite(ref).all()
+    assert np.array_equal(got, ref, equal_nan=True)
 
 
 def test_grad_cam_resized(dev):
