@@ -552,9 +552,47 @@ def measure_matmul(n, args, dev):
     return entry
 
 
-def host_path(name, dev):
+def copy_rates(arrays, dev, reps=3):
+    """Seconds to copy `arrays` (host numpy arrays) to the device and back,
+    from pageable memory (numpy's) and from pinned memory: the median of
+    `reps`, and the GB/s."""
+    import numpy as np
+    import torch
+    nbytes = sum(a.nbytes for a in arrays)
+    out = {}
+    for kind in ("pageable", "pinned"):
+        hosts = [torch.from_numpy(a) for a in arrays]
+        if kind == "pinned":
+            hosts = [h.pin_memory() for h in hosts]
+        devs = [torch.empty(h.shape, device=dev, dtype=h.dtype) for h in hosts]
+        th, td = [], []
+        for _ in range(reps + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for d, h in zip(devs, hosts):
+                d.copy_(h, non_blocking=kind == "pinned")
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for d, h in zip(devs, hosts):
+                h.copy_(d, non_blocking=kind == "pinned")
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            th.append(t1 - t0)
+            td.append(t2 - t1)
+        h2d, d2h = float(np.median(th[1:])), float(np.median(td[1:]))
+        out[kind] = {"h2d_gbps": round(nbytes / h2d / 1e9, 1),
+                     "d2h_gbps": round(nbytes / d2h / 1e9, 1)}
+        del hosts, devs
+    out["bytes_per_copy"] = nbytes
+    return out
+
+
+def host_path(name, dev, kernel_us):
     """The drop-in host-buffer entry points (katsu_amd.host): each pass copies
-    its operands in and its result out over PCIe."""
+    its operands in and its result out over PCIe.  Beside the time per step:
+    the bytes each direction moves, the box's pageable and pinned copy rates
+    for the same arrays (torch copies, no kernel), and the step's kernel time
+    from the device-resident timings, so the copy share is visible."""
     import numpy as np
 
     from katsu_amd import host, synth
@@ -562,8 +600,8 @@ def host_path(name, dev):
     st, pad = cfg["stride"], cfg["pad"]
     x, w = synth.conv_inputs(cfg)
     gh = np.ones(synth.out_shape(cfg), np.float32)
-    host.conv2d_forward(x, w, st, pad)  # warm the staging pool
-    host.conv2d_backward(x, w, gh, st, pad)
+    y = host.conv2d_forward(x, w, st, pad)  # warm the staging pool
+    dx, dw = host.conv2d_backward(x, w, gh, st, pad)
     reps = 3
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -573,10 +611,22 @@ def host_path(name, dev):
         host.conv2d_backward(x, w, gh, st, pad)
     t2 = time.perf_counter()
     f_ms, b_ms = (t1 - t0) / reps * 1e3, (t2 - t1) / reps * 1e3
+    # Forward: x, w in, y out; backward: x, w, G in, dX, dW out.
+    h2d_bytes = 2 * x.nbytes + 2 * w.nbytes + gh.nbytes
+    d2h_bytes = y.nbytes + dx.nbytes + dw.nbytes
+    rates = copy_rates([x, gh], dev)
+    pg, pn = rates["pageable"], rates["pinned"]
+    est = lambda r: (h2d_bytes / (r["h2d_gbps"] * 1e9) + d2h_bytes / (r["d2h_gbps"] * 1e9)) * 1e3
     return {"ms_per_step": round(f_ms + b_ms, 3), "fwd_ms": round(f_ms, 3),
             "bwd_ms": round(b_ms, 3),
             "tflops": round(3 * synth.conv_flops(cfg) / ((f_ms + b_ms) * 1e-3) / 1e12, 3),
-            "note": "host-pointer ABI, PCIe copies included"}
+            "h2d_bytes": h2d_bytes, "d2h_bytes": d2h_bytes,
+            "kernel_ms": round(kernel_us / 1e3, 4),
+            "copy_rates": rates,
+            "copies_at_pageable_rate_ms": round(est(pg), 3),
+            "copies_at_pinned_rate_ms": round(est(pn), 3),
+            "note": ("host-pointer ABI, PCIe copies included; copy rates are torch copies of "
+                     "x and G of this workload on this box")}
 
 
 def main():
@@ -654,7 +704,8 @@ def main():
         out["matmul"] = {str(n): measure_matmul(n, args, dev) for n in args.matmul_n}
 
     if not args.no_host:
-        out["host_buffer_path"] = host_path(args.workload, dev)
+        out["host_buffer_path"] = host_path(
+            args.workload, dev, head["kernels"]["fwd"]["avg_us"] + head["kernels"]["bwd"]["avg_us"])
         # The C++ front end (the reference's public API) with device-resident
         # tensors: forward + sum + backward through Conv2D at config 3, matmul
         # + sum + backward at 1024, the config-5 chain, end to end (a child

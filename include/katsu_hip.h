@@ -17,7 +17,11 @@
  * Two families of entry points:
  *   - host-pointer ("drop-in") entry points take the caller's host buffers,
  *     as the reference's slices are, copy them to the device, run on the
- *     library's stream and return once the outputs are written back;
+ *     library's stream and return once the outputs are written back.  Copies
+ *     of 1 MiB or more go through a ring of four pinned 8 MiB host chunks
+ *     (allocated on first use, freed by katsu_hip_shutdown), the CPU side of
+ *     each chunk split over four threads (environment: KATSU_COPY_THREADS,
+ *     KATSU_COPY_CHUNK_MB); the caller's buffers stay pageable;
  *   - *_dev entry points take device pointers and a hipStream_t (passed as
  *     void*, 0 = the null stream) and return right after the launch.
  *

@@ -23,6 +23,7 @@
 #include "direct.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
+#include "hostcopy.hpp"
 #include "pointwise.hpp"
 #include "smallc.hpp"
 #include "stemdx.hpp"
@@ -64,6 +65,7 @@ struct State {
     int device = -1;
     hipStream_t stream = nullptr;
     Buffer staging[5];
+    HostCopy copy;  // the host-pointer entry points' pinned staging ring
     Pool pool;
 };
 
@@ -2437,7 +2439,13 @@ int h2d(Buffer &b, const float *src, size_t count, hipStream_t st) {
     int rc = ensure(b, bytes);
     if (rc != KATSU_OK) return rc;
     if (bytes == 0) return KATSU_OK;
-    return map_hip(hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, st));
+    return map_hip(state().copy.h2d(b.ptr, src, bytes, st));
+}
+
+// Device to host after the work ordered on st, returning once dst holds it.
+int d2h(float *dst, const Buffer &b, size_t count, hipStream_t st) {
+    const size_t bytes = count * sizeof(float);
+    return bytes ? map_hip(state().copy.d2h(dst, b.ptr, bytes, st)) : KATSU_OK;
 }
 
 // beta*C for an empty reduction on a host buffer (beta is 0 or 1).
@@ -2447,12 +2455,8 @@ int host_scale(float *c, size_t count, float beta) {
 }
 
 int d2h_sync(float *dst, const Buffer &b, size_t count, hipStream_t st) {
-    const size_t bytes = count * sizeof(float);
-    if (bytes) {
-        int rc = map_hip(hipMemcpyAsync(dst, b.ptr, bytes, hipMemcpyDeviceToHost, st));
-        if (rc != KATSU_OK) return rc;
-    }
-    return map_hip(hipStreamSynchronize(st));
+    const int rc = d2h(dst, b, count, st);
+    return rc != KATSU_OK ? rc : map_hip(hipStreamSynchronize(st));
 }
 
 }  // namespace
@@ -2488,6 +2492,7 @@ void katsu_hip_shutdown(void) {
     std::lock_guard<std::mutex> lock(s.mu);
     if (!s.ready) return;
     (void)hipStreamSynchronize(s.stream);
+    s.copy.release();
     for (Buffer &b : s.staging) {
         if (b.ptr) (void)hipFree(b.ptr);
         b = Buffer{};
@@ -2681,11 +2686,7 @@ int katsu_hip_conv2d_bwd_f32(const float *x, const float *w, const float *gy, fl
                       WsSource{nullptr, 0, true}, s.stream);
     if (rc) return rc;
     if (same) return d2h_sync(dx, s.staging[3], nx, s.stream);
-    if (nx > 0) {
-        rc = map_hip(hipMemcpyAsync(dx, s.staging[3].ptr, nx * sizeof(float),
-                                    hipMemcpyDeviceToHost, s.stream));
-        if (rc) return rc;
-    }
+    if ((rc = d2h(dx, s.staging[3], nx, s.stream))) return rc;
     return d2h_sync(dw, s.staging[4], nw, s.stream);
 }
 
