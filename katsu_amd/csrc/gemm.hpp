@@ -487,6 +487,206 @@ __global__ void __launch_bounds__(64 * KS, OCC) gemm_rd_kernel(const GemmArgs g)
     gemm_rd_block<TA, TB, KS, NKB, D>(g, blockIdx.x, gridDim.x);
 }
 
+// One 64 x 64 tile of a register-direct problem, as gemm_rd_block lays it
+// out: its operand resources, the lane parts of its operand offsets and
+// their per-k-block advance.
+template <bool TA, bool TB, int NKB>
+struct RdTile {
+    __amdgpu_buffer_rsrc_t ra, rb;
+    int va[4], vb[4];
+    int sa, sbk, a_k0, b_k0, i0, j0;
+
+    __device__ __forceinline__ void init(const GemmArgs &g, int tile, int w, int lane) {
+        const int l16 = lane & 15, g4 = lane >> 4;
+        const int gsz = g.gm * g.tiles_n, grp = tile / gsz, gi = tile - grp * gsz;
+        i0 = (grp * g.gm + gi % g.gm) * 64;
+        j0 = (gi / g.gm) * 64;
+        const int kb0 = w * NKB * 16;
+        ra = buf_rsrc(g.a, g.a_bytes);
+        rb = buf_rsrc(g.b, g.b_bytes);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (!TA) {
+                const int i = i0 + 16 * q + l16;
+                va[q] = i < g.M ? (i * g.lda + 4 * g4) * 4 : kOOB;
+            } else {
+                const int i = i0 + 4 * l16;
+                va[q] = i < g.M ? ((4 * g4 + q) * g.lda + i) * 4 : kOOB;
+            }
+            if (TB) {
+                const int j = j0 + 16 * q + l16;
+                vb[q] = j < g.N ? (j * g.ldb + 4 * g4) * 4 : kOOB;
+            } else {
+                const int j = j0 + 4 * l16;
+                vb[q] = j < g.N ? ((4 * g4 + q) * g.ldb + j) * 4 : kOOB;
+            }
+        }
+        sa = TA ? 16 * g.lda * 4 : 64;
+        sbk = TB ? 64 : 16 * g.ldb * 4;
+        a_k0 = TA ? kb0 * g.lda * 4 : kb0 * 4;
+        b_k0 = TB ? kb0 * 4 : kb0 * g.ldb * 4;
+    }
+    // The eight 16-byte loads of k-block kblk: dst[0][q] A, dst[1][q] B.
+    __device__ __forceinline__ void fetch(floatx4 (&dst)[2][4], int kblk) const {
+        const int oa = a_k0 + kblk * sa, ob = b_k0 + kblk * sbk;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dst[0][q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[q], oa, 0));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dst[1][q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rb, vb[q], ob, 0));
+    }
+};
+
+// The 64 MFMAs of one k-block (gemm_rd_block's order).
+template <bool TA, bool TB>
+__device__ __forceinline__ void rd_mma(floatx4 (&acc)[4][4], const floatx4 (&cur)[2][4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float av = TA ? cur[0][s][a] : cur[0][a][s];
+                const float bv = TB ? cur[1][b][s] : cur[1][s][b];
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[a][b], 0, 0, 0);
+            }
+}
+
+// The KS waves' sums added through LDS in wave order and stored, as at the
+// end of gemm_rd_block (KS > 1).
+template <bool TA, bool TB, int KS>
+__device__ __forceinline__ void rd_store(const GemmArgs &g, const floatx4 (&acc)[4][4], int i0,
+                                         int j0, int w, int lane, float *part) {
+    const int l16 = lane & 15, g4 = lane >> 4;
+    auto put = [&](int a, int v, const float *val) __attribute__((always_inline)) {
+        const int m = 4 * g4 + v;
+        const int i = TA ? i0 + 4 * m + a : i0 + 16 * a + m;
+        if (i >= g.M) return;
+        float *row = g.c + (int64_t)i * g.ldc;
+        if (!TB) {
+            const int j = j0 + 4 * l16;
+            if (j >= g.N) return;
+            floatx4 r = floatx4{val[0], val[1], val[2], val[3]};
+            floatx4 *d = reinterpret_cast<floatx4 *>(row + j);
+            if (g.beta != 0.f) r += *d;
+            *d = r;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = j0 + 16 * b + l16;
+                if (j < g.N) row[j] = g.beta != 0.f ? row[j] + val[b] : val[b];
+            }
+        }
+    };
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                part[(w * 64 + (a * 4 + v) * 4 + b) * 64 + lane] = acc[a][b][v];
+    __syncthreads();
+    constexpr int GPW = 16 / KS;
+#pragma unroll
+    for (int e = 0; e < GPW; ++e) {
+        const int av = w * GPW + e, a = av >> 2, v = av & 3;
+        float val[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            float t = part[(av * 4 + b) * 64 + lane];
+#pragma unroll
+            for (int p = 1; p < KS; ++p) t += part[(p * 64 + av * 4 + b) * 64 + lane];
+            val[b] = t;
+        }
+        put(a, v, val);
+    }
+}
+
+// The matmul VJP's dA (NT, nt) and dB (TN, tn) tiles of the same index in
+// one block, one after the other: the loads of dB's first D k-blocks are
+// issued during dA's last D k-blocks (the ring of loads in flight runs on
+// from one product into the next), so the second tile starts without a
+// load round trip, and dA's store epilogue overlaps dB's first loads.  Each
+// tile's loads, MFMAs and wave-order sum are those of gemm_rd_block, so the
+// bits are those of the two products computed apart.  Both problems have
+// the same tile grid (nb tiles).
+template <int KS, int NKB, int D>
+__device__ __forceinline__ void gemm_rd_pair_block(const GemmArgs &nt, const GemmArgs &tn, int bid,
+                                                   int nb) {
+    static_assert(KS > 1, "the waves' sums go through LDS");
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = xcd_swizzle(bid, nb);
+    extern __shared__ float part[];
+    RdTile<false, true, NKB> t0;
+    RdTile<true, false, NKB> t1;
+    t0.init(nt, tile, w, lane);
+    t1.init(tn, tile, w, lane);
+
+    floatx4 fr[D][2][4];
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < D && p < NKB; ++p) t0.fetch(fr[p], p);
+    // dA: k-block kb sits in slot kb % D; the refill of its slot is block
+    // kb + D of dA, or past dA's end, block kb + D - NKB of dB.
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        floatx4 cur[2][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cur[0][q] = fr[kb % D][0][q];
+            cur[1][q] = fr[kb % D][1][q];
+        }
+        if (kb + D < NKB)
+            t0.fetch(fr[kb % D], kb + D);
+        else if (kb + D - NKB < NKB)
+            t1.fetch(fr[kb % D], kb + D - NKB);
+        rd_mma<false, true>(acc, cur);
+        __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);   // the refill
+        __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);  // then the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    rd_store<false, true, KS>(nt, acc, t0.i0, t0.j0, w, lane, part);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // dB: k-block kb sits in slot (NKB + kb) % D.
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        constexpr int kOff = NKB % D;
+        const int slot = (kOff + kb) % D;
+        floatx4 cur[2][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cur[0][q] = fr[slot][0][q];
+            cur[1][q] = fr[slot][1][q];
+        }
+        const bool refill = kb + D < NKB;
+        if (refill) t1.fetch(fr[slot], kb + D);
+        rd_mma<true, false>(acc, cur);
+        if (refill) __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // dA's sums in LDS may still be read by a wave that is behind.
+    __syncthreads();
+    rd_store<true, false, KS>(tn, acc, t1.i0, t1.j0, w, lane, part);
+}
+
+template <int KS, int NKB, int D>
+__global__ void __launch_bounds__(64 * KS, 1)
+    gemm_rd_vjp_pair_kernel(const GemmArgs nt, const GemmArgs tn) {
+    gemm_rd_pair_block<KS, NKB, D>(nt, tn, blockIdx.x, gridDim.x);
+}
+
 // The matmul VJP's dA (NT) and dB (TN) in one register-direct launch (see
 // gemm_vjp_kernel for the block split).
 template <int KS, int NKB, int D, int OCC>

@@ -379,13 +379,16 @@ bool gemm_fast_plan(const float *a, const float *b, const float *c, int64_t M, i
 #define KATSU_GEMM_RD_D 3
 #endif
 #ifndef KATSU_GEMM_RD_VJP_D
-#define KATSU_GEMM_RD_VJP_D 3
+#define KATSU_GEMM_RD_VJP_D 2
 #endif
 #ifndef KATSU_GEMM_RD_KS
 #define KATSU_GEMM_RD_KS 4
 #endif
 #ifndef KATSU_GEMM_RD_VJP_KS
 #define KATSU_GEMM_RD_VJP_KS 4
+#endif
+#ifndef KATSU_GEMM_RD_VJP_PAIR
+#define KATSU_GEMM_RD_VJP_PAIR 1  // square VJPs: a block takes a dA tile, then a dB tile
 #endif
 #ifndef KATSU_GEMM_RD_VJP_OCC
 #define KATSU_GEMM_RD_VJP_OCC 1  // blocks per CU the VJP kernel is built for
@@ -543,6 +546,16 @@ int matmul_vjp_dev(const float *a, const float *b, const float *g, float *da, fl
             ra.c = da;
             rb.c = db;
             const int nb0 = ra.tiles_m * ra.tiles_n, nb1 = rb.tiles_m * rb.tiles_n;
+            if (KATSU_GEMM_RD_VJP_PAIR && nb0 == nb1) {
+                // One block per tile index: its dA tile, then its dB tile.
+                constexpr auto pk =
+                    gemm_rd_vjp_pair_kernel<kRdVjpKs, kRdVjpNkb, KATSU_GEMM_RD_VJP_D>;
+                constexpr size_t lds = kRdVjpKs * 64 * 64 * 4;
+                const int rc = lds_optin<pk>(lds);
+                if (rc != KATSU_OK) return rc;
+                pk<<<dim3((unsigned)nb0), dim3(64 * kRdVjpKs), lds, st>>>(ra, rb);
+                return launch_status();
+            }
             constexpr auto kern =
                 gemm_rd_vjp_kernel<kRdVjpKs, kRdVjpNkb, KATSU_GEMM_RD_VJP_D, KATSU_GEMM_RD_VJP_OCC>;
             constexpr size_t lds = kRdVjpKs * 64 * 64 * 4;
