@@ -35,6 +35,13 @@
 
 namespace katsu {
 
+// Wave-group forward blocks (KG > 1) read the fragments of k-step kk+1
+// during step kk's MFMAs when they have at most this many fragments per
+// wave, else one step at a time.
+#ifndef KATSU_FWD_KG_PIPE_F
+#define KATSU_FWD_KG_PIPE_F 8
+#endif
+
 // Scheduling fence for a software-pipelined k-step: the LDS reads of the
 // next step (NREAD of them) are issued before the MFMAs of the current step
 // (NMFMA), so the reads' latency overlaps the MFMAs.  Without it the
@@ -194,8 +201,9 @@ struct Dxs2Taps {
     static_assert(NO <= 16 && NP == R * S, "every tap in exactly one (offset, phase) pair");
 };
 
-// LDS layout (floats) of the forward kernel.
-template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE>
+// LDS layout (floats) of the forward kernel (KG: groups of four waves, see
+// direct_fwd_block).
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int KG = 1>
 struct DirectFwdGeo {
     static constexpr int RS = R * S;
     static_assert(PITCH == 32 || PITCH % 64 == 0, "halo row pitch: 32 or a multiple of 64");
@@ -206,14 +214,14 @@ struct DirectFwdGeo {
     //   WMODE 0, 2: KT rows (co) of CB*RS floats, pitch CB*RS + 4
     //   WMODE 1, 3: CB rows (ci) of KT*RS floats, pitch == 16 (mod 32)
     // Pitches are multiples of 4 floats so 16-byte DMA lands on row
-    // boundaries.  The region is a whole number of 1024 floats, so each of
-    // the 4 waves issues the same number of loads for it (16-byte or 4-byte),
-    // without a per-wave branch; loads past the last row read zeros.
+    // boundaries.  The region is a whole number of 1024*KG floats, so each
+    // of the 4*KG waves issues the same number of loads for it (16-byte or
+    // 4-byte), without a per-wave branch; loads past the last row read zeros.
     static constexpr bool WBYCI = WMODE == 1 || WMODE == 3;  // weight rows per input channel
     static constexpr int WROWS = WBYCI ? CB : KT;
     static constexpr int WLEN = WBYCI ? KT * RS : CB * RS;
     static constexpr int WPITCH = WBYCI ? WLEN + ((16 - WLEN % 32) + 32) % 32 : WLEN + 4;
-    static constexpr int WS = (WROWS * WPITCH + 1023) / 1024 * 1024;
+    static constexpr int WS = (WROWS * WPITCH + 1024 * KG - 1) / (1024 * KG) * (1024 * KG);
     static_assert(WLEN % 4 == 0 && WPITCH % 4 == 0, "weight rows of whole float4");
     static constexpr int STAGE = XS + WS;
     // Output transpose buffer (reuses the stages after the last chunk).
@@ -251,7 +259,7 @@ struct DirectFwdGeo {
 // real G).  (oy, ox) is the output pixel of the kernel's own problem, (iy,
 // ix) the full-resolution dX pixel of the stride-2 forms.  Taken only for
 // non-finite data, so it is written for clarity, not speed.
-template <int KT, int R, int S, int WMODE, int EPI, int PD>
+template <int KT, int R, int S, int WMODE, int EPI, int PD, int NW = 4>
 __device__ __forceinline__ void direct_fwd_epilogue_exact(const DirectArgs &a, const float *ys,
                                                        int ypitch, float *outb, int n, int p0,
                                                        int np, int co0, int wave, int lane) {
@@ -272,7 +280,7 @@ __device__ __forceinline__ void direct_fwd_epilogue_exact(const DirectArgs &a, c
                             ox);
         return exact_dx(in_img, a.w, a.CI, a.CO, a.H, a.W, R, S, 2, PD, co, iy, ix);
     };
-    for (int row = wave; row < KT; row += 4) {
+    for (int row = wave; row < KT; row += NW) {
         const int co = co0 + row;
         if (co >= a.CO) break;
         if (EPI == 3) {
@@ -309,13 +317,25 @@ __device__ __forceinline__ void direct_fwd_epilogue_exact(const DirectArgs &a, c
     }
 }
 
+//
+// KG (groups of four waves, forward and stride-1 dX only): the block runs
+// 4*KG waves, and wave group g takes channel quads g, g+KG, ... of every
+// stage, so each group covers the whole tile over 1/KG of the reduction.
+// The LDS stages are shared, so a block of 8 waves needs no more LDS than
+// one of 4, and two blocks per CU keep four waves per SIMD (against two):
+// MFMA issue from more waves per SIMD hides the gaps between one wave's
+// back-to-back MFMAs.  The groups' sums are added in group order in the
+// epilogue's LDS transpose.
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool WVEC, bool S2 = false, bool RF = false, int PD = 0>
+          bool WVEC, bool S2 = false, bool RF = false, int PD = 0, int KG = 1>
 __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>;
     constexpr int RS = R * S;
-    constexpr int WOC = KT / 16;            // waves along output channels
-    constexpr int CPW = CB / 4;             // input channels staged per wave
+    constexpr int NW = 4 * KG;              // waves
+    constexpr int WOC = KT / 16;            // waves of a group along output channels
+    constexpr int CPW = CB / NW;            // input channels staged per wave
+    static_assert(CB % NW == 0 && (CB / 4) % KG == 0, "whole channel quads per wave group");
+    static_assert(KG == 1 || WMODE <= 1, "wave groups: forward and stride-1 dX");
     constexpr int RPL = PITCH >= 64 ? 1 : 64 / PITCH;   // halo rows per wave load
     constexpr int LPR = PITCH >= 64 ? PITCH / 64 : 1;   // wave loads per halo row
     static_assert(KT % 16 == 0 && 4 % WOC == 0, "KT must be 16, 32 or 64");
@@ -328,7 +348,8 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     extern __shared__ float smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int woc = wave % WOC, wpx = wave / WOC;
+    const int w4 = KG == 1 ? wave : wave & 3, kg = KG == 1 ? 0 : wave >> 2;  // wave in group, group
+    const int woc = w4 % WOC, wpx = w4 / WOC;
 
     const int t = xcd_swizzle(bid, nb);
     const int cob = t % a.co_blocks;
@@ -349,15 +370,17 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         p = p < p1 ? p : p0;
         const int oy = a.fd_ow.div(p);
         const int ox = p - oy * a.OW;
-        pix[f] = (lane >> 4) * Geo::CPITCH + (oy - oy0) * a.st * PITCH + (S2 ? ox : ox * a.st);
+        pix[f] = (KG == 1 ? lane >> 4 : 4 * kg + (lane >> 4)) * Geo::CPITCH +
+                 (oy - oy0) * a.st * PITCH + (S2 ? ox : ox * a.st);
     }
-    // Per-lane A-fragment base: row co = woc*16 + l%16, channel l/16.
+    // Per-lane A-fragment base: row co = woc*16 + l%16, channel 4*kg + l/16.
     const int abase = Geo::WBYCI
-        ? (lane >> 4) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS
-        : (woc * 16 + (lane & 15)) * Geo::WPITCH + (lane >> 4) * RS;
+        ? (4 * kg + (lane >> 4)) * Geo::WPITCH + (woc * 16 + (lane & 15)) * RS
+        : (woc * 16 + (lane & 15)) * Geo::WPITCH + (4 * kg + (lane >> 4)) * RS;
+    int abase_l = abase;  // LEAN: moves with the stage
 
     // ---- staging: LDS-direct loads ------------------------------------------
-    // Input halo: wave w stages channels w + 4j (j < CPW), one 64-float run
+    // Input halo: wave w stages channels w + NW*j (j < CPW), one 64-float run
     // per load (a row chunk, or two 32-float rows).  Weights: 16-byte loads
     // when every float4 of a row lies inside the row (WVEC), else 4-byte
     // loads (WMODE 2: gathered through a per-lane table).  Padding, rows past
@@ -397,33 +420,46 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
 
     // Per-lane byte offsets of the stage loads for the chunk at ci0 = 0; a
     // chunk adds a uniform delta.  A kOOB-based offset (< 2^31 with the
-    // image below 1 GiB) stays out of range after the delta.
-    uint32_t in_off[CPW][ROWS / RPL][LPR];
+    // image below 1 GiB) stays out of range after the delta.  Kept in
+    // registers, or with wave groups (LEAN: 128 VGPRs at four waves per
+    // SIMD) recomputed at each load (halo_off, wload), a few VALU operations
+    // per load.
+    constexpr bool LEAN = KG > 1;
+    uint32_t in_off[LEAN ? 1 : CPW][LEAN ? 1 : ROWS / RPL][LPR];
+    if (!LEAN) {
 #pragma unroll
-    for (int j = 0; j < CPW; ++j)
+        for (int j = 0; j < CPW; ++j)
 #pragma unroll
-        for (int r = 0; r < ROWS; r += RPL) {
-            const int iy = iy0 + r + lrow;
-            const bool ok = (unsigned)iy < (unsigned)a.H;
+            for (int r = 0; r < ROWS; r += RPL) {
+                const int iy = iy0 + r + lrow;
+                const bool ok = (unsigned)iy < (unsigned)a.H;
 #pragma unroll
-            for (int c = 0; c < LPR; ++c)
-                in_off[j][r / RPL][c] =
-                    ok ? (uint32_t)(((wv + 4 * j) * a.H + iy) * a.W * 4) + (uint32_t)colb[c]
-                       : (uint32_t)kOOB;
-        }
-    // Weights (WMODE 0, 1): wave load i = 4q + wv of the weight region; the
+                for (int c = 0; c < LPR; ++c)
+                    in_off[j][r / RPL][c] =
+                        ok ? (uint32_t)(((wv + NW * j) * a.H + iy) * a.W * 4) + (uint32_t)colb[c]
+                           : (uint32_t)kOOB;
+            }
+    }
+    auto halo_off = [&](int j, int r, int c) __attribute__((always_inline)) {
+        const int iy = iy0 + r + lrow;
+        const bool ok = (unsigned)iy < (unsigned)a.H;
+        return ok ? (uint32_t)(((wv + NW * j) * a.H + iy) * a.W * 4) + (uint32_t)colb[c]
+                  : (uint32_t)kOOB;
+    };
+    // Weights (WMODE 0, 1): wave load i = NW*q + wv of the weight region; the
     // lane's row and column in it, the offset at ci0 = 0, and whether the row
     // exists apart from the chunk's channel count.
     constexpr int WE = WVEC ? 4 : 1;                  // floats per lane per load
     constexpr int WNI = Geo::WS / (64 * WE);          // wave loads
-    constexpr int WNQ = (WNI + 3) / 4;
-    uint32_t w_off[WMODE == 2 ? 1 : WNQ];
-    int w_col[WMODE == 2 ? 1 : WNQ], w_row[WMODE == 2 ? 1 : WNQ];
-    bool w_ok[WMODE == 2 ? 1 : WNQ];
-    if (WMODE != 2) {
+    constexpr int WNQ = (WNI + NW - 1) / NW;
+    constexpr int WNQK = WMODE == 2 || LEAN ? 1 : WNQ;
+    uint32_t w_off[WNQK];
+    int w_col[WNQK], w_row[WNQK];
+    bool w_ok[WNQK];
+    if (WMODE != 2 && !LEAN) {
 #pragma unroll
         for (int q = 0; q < WNQ; ++q) {
-            const int e = ((q * 4 + wv) * 64 + lane) * WE;
+            const int e = ((q * NW + wv) * 64 + lane) * WE;
             const int row = e / Geo::WPITCH, col = e - (e / Geo::WPITCH) * Geo::WPITCH;
             w_row[q] = row;
             w_col[q] = col;
@@ -438,6 +474,22 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             }
         }
     }
+    // LEAN: weight load q's offset at ci0 = 0 and its checks, as above.
+    auto wload = [&](int q, uint32_t &off, int &col, int &row, bool &ok)
+        __attribute__((always_inline)) {
+        const int e = ((q * NW + wv) * 64 + lane) * WE;
+        row = e / Geo::WPITCH;
+        col = e - row * Geo::WPITCH;
+        if (WMODE == 0) {
+            const int co = co0 + row;
+            ok = row < KT && co < a.CO;
+            off = (uint32_t)((co * a.CI * RS + col) * 4);
+        } else {
+            const int lim = min(KT, a.CO - co0) * RS;
+            ok = row < CB && col < lim;
+            off = (uint32_t)(((row * a.CO + co0) * RS + col) * 4);
+        }
+    };
 
     // Load i of a stage (NSTG per wave): halo loads first, then weight loads.
     // Issued one or two per k-step inside the previous chunk's MFMA loop
@@ -445,10 +497,11 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     // chunk boundary.  ci0 >= CI makes every load read zeros, which is how
     // the last chunk's loop runs.
     constexpr int NHALO = CPW * (ROWS / RPL) * LPR;
-    constexpr int NWL = WMODE == 2 ? Geo::WS / 256 : Geo::WS / (256 * WE);
+    constexpr int NWL = WMODE == 2 ? Geo::WS / 256 : Geo::WS / (64 * NW * WE);
     constexpr int NSTG = NHALO + NWL;
-    static_assert(NSTG <= 4 * (CB / 4) * RS, "at most 4 loads per k-step");
-    static_assert(WMODE == 2 ? (Geo::WS / 64) % 4 == 0 : WNI % 4 == 0, "equal loads per wave");
+    constexpr int NKW = (CB / 4 / KG) * RS;  // k-steps of a wave per stage
+    static_assert(NSTG <= 4 * NKW, "at most 4 loads per k-step");
+    static_assert(WMODE == 2 ? (Geo::WS / 64) % 4 == 0 : WNI % NW == 0, "equal loads per wave");
     auto stage_part = [&](float *stage, int ci0, int i) __attribute__((always_inline)) {
         if (i < NHALO) {
             const int j = i / ((ROWS / RPL) * LPR);
@@ -458,12 +511,17 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             // selected, so the load is not split into branches on the
             // (uniform) channel test.
             const uint32_t din = (uint32_t)ci0 * (uint32_t)(a.H * a.W * 4);
-            const uint32_t oob = (uint32_t)(ci0 + wv + 4 * j >= a.CI) << 31;
-            lds_dma_b32(rin, stage + (wv + 4 * j) * Geo::CPITCH + r * PITCH + c * 64,
-                        (int)((in_off[j][r / RPL][c] + din) | oob));
+            const uint32_t oob = (uint32_t)(ci0 + wv + NW * j >= a.CI) << 31;
+            uint32_t off;
+            if constexpr (LEAN)
+                off = halo_off(j, r, c);
+            else
+                off = in_off[j][r / RPL][c];
+            lds_dma_b32(rin, stage + (wv + NW * j) * Geo::CPITCH + r * PITCH + c * 64,
+                        (int)((off + din) | oob));
             return;
         }
-        const int q = i - NHALO, wi = q * 4 + wv;  // this wave's load q: wave load wi
+        const int q = i - NHALO, wi = q * NW + wv;  // this wave's load q: wave load wi
         float *wst = stage + Geo::XS;
         if (WMODE == 2) {
             lds_dma_b32(rw, wst + wi * 64, wtab[q] >= 0 ? (wtab[q] + ci0 * a.g_crs) * 4 : kOOB);
@@ -472,9 +530,19 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         // WMODE 0: the chunk's valid columns; WMODE 1, 3: the chunk's channels.
         const uint32_t dw = WMODE == 0 ? (uint32_t)(ci0 * RS * 4) : (uint32_t)(ci0 * a.CO * RS * 4);
         const int lim = WMODE == 0 ? min(CB, a.CI - ci0) * RS : 0;
-        const bool ok = WMODE == 0 ? (w_ok[q] && w_col[q] < lim)
-                                   : (w_ok[q] && ci0 + w_row[q] < a.CI);
-        const int off = ok ? (int)(w_off[q] + dw) : kOOB;
+        int off;
+        if constexpr (LEAN) {
+            uint32_t o;
+            int col, row;
+            bool wok;
+            wload(q, o, col, row, wok);
+            const bool ok = WMODE == 0 ? (wok && col < lim) : (wok && ci0 + row < a.CI);
+            off = ok ? (int)(o + dw) : kOOB;
+        } else {
+            const bool ok = WMODE == 0 ? (w_ok[q] && w_col[q] < lim)
+                                       : (w_ok[q] && ci0 + w_row[q] < a.CI);
+            off = ok ? (int)(w_off[q] + dw) : kOOB;
+        }
         if (WVEC)
             lds_dma_b128(rw, wst + wi * 256, off);
         else
@@ -501,13 +569,15 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
 #pragma unroll
     for (int f = 0; f < F; ++f) acc[f] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // One k-step kk = (channel quad cs, tap): the A fragment and the F B
-    // fragments it multiplies.  All offsets are compile-time after unrolling.
+    // One k-step kk = (the wave's channel quad cs, tap): the A fragment and
+    // the F B fragments it multiplies.  The group's first quad is in the
+    // lane bases; its quads are KG apart.  All offsets are compile-time
+    // after unrolling.
     auto fetch = [&](const float *base, const int kk, float (&b)[F], float &av)
         __attribute__((always_inline)) {
-        const int cs = kk / RS, tap = kk % RS;
+        const int cs = kk / RS * KG, tap = kk % RS;
         const int r = tap / S, s = tap % S;
-        const float *ws = base + Geo::XS + abase;
+        const float *ws = base + Geo::XS + (LEAN ? abase_l : abase);
         av = WMODE == 1 ? ws[cs * 4 * Geo::WPITCH + (RS - 1 - tap)] : ws[cs * 4 * RS + tap];
         const int toff = cs * 4 * Geo::CPITCH + r * PITCH + (S2 ? (s & 1) * HALF + (s >> 1) : s);
 #pragma unroll
@@ -583,7 +653,21 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             compute3(base, nxt, ci0n);
             return;
         }
-        constexpr int NK = (CB / 4) * RS;
+        constexpr int NK = NKW;
+        if constexpr (KG > 1 && F > KATSU_FWD_KG_PIPE_F) {
+            // Wide tiles: one register set keeps the wave within the VGPRs
+            // of its occupancy, and the other waves of the SIMD hide its
+            // LDS latency.
+            float b0[F], a0;
+#pragma unroll
+            for (int kk = 0; kk < NK; ++kk) {
+                fetch(base, kk, b0, a0);
+                mma(b0, a0);
+                stage_step(nxt, ci0n, kk, NK);
+                order_step<F + 1, F>(nsteploads(kk, NK));
+            }
+            return;
+        }
         float b0[F], b1[F];
         float a0, a1;
         fetch(base, 0, b0, a0);
@@ -613,7 +697,22 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     stage_in(st0, 0);
     wait_lds_dma();
     __syncthreads();
-    for (int ch = 0; ch < nch; ch += 2) {
+    if constexpr (LEAN) {
+        // One loop body: the lane bases move to the other stage after each
+        // chunk, which keeps the accumulators in place across the loop's
+        // back edge (the unrolled form needs registers to carry them).
+        for (int ch = 0; ch < nch; ++ch) {
+            const bool odd = ch & 1;
+            compute(smem, odd ? st0 : st1, ch + 1 < nch ? (ch + 1) * CB : a.CI);
+            wait_lds_dma();
+            __syncthreads();
+            const int d = odd ? -Geo::STAGE : Geo::STAGE;
+#pragma unroll
+            for (int f = 0; f < F; ++f) pix[f] += d;
+            abase_l += d;
+        }
+    }
+    for (int ch = 0; ch < (LEAN ? 0 : nch); ch += 2) {
         compute(st0, st1, ch + 1 < nch ? (ch + 1) * CB : a.CI);
         wait_lds_dma();
         __syncthreads();
@@ -628,9 +727,19 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     // run -- contiguous in NCHW -- as 16-byte stores (EPI 0), or scatter each
     // super-pixel channel to its full-resolution positions (EPI 1).
     // Phase ph of WMODE 3 takes rows ph*KT .. ph*KT + KT-1 of ys.
+    // With wave groups, group 0 stores its sums and each later group adds
+    // its own in turn (a barrier apart), keeping the result in registers.
     float *ys = smem;
-    auto put = [&](int ph, const floatx4 (&ac)[F]) __attribute__((always_inline)) {
+    auto put = [&](int ph, floatx4 (&ac)[F], const bool add) __attribute__((always_inline)) {
         float *yp = ys + ph * KT * Geo::YPITCH;
+        auto one = [&](floatx4 &q, const int v, const int e) __attribute__((always_inline)) {
+            if (KG == 1) {
+                yp[e] = q[v];
+                return;
+            }
+            if (add) q[v] = yp[e] + q[v];
+            yp[e] = q[v];
+        };
         if (RF) {
             // Pixel p0 + row*OW + col sits at ys column row*OW + col.
             if ((lane & 15) < a.OW) {
@@ -638,24 +747,30 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                 for (int f = 0; f < F; ++f)
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        yp[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * a.OW +
-                           (lane & 15)] = ac[f][v];
+                        one(ac[f], v, (woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH +
+                                          (wpx * F + f) * a.OW + (lane & 15));
             }
         } else {
 #pragma unroll
             for (int f = 0; f < F; ++f)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    yp[(woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH + (wpx * F + f) * 16 +
-                       (lane & 15)] = ac[f][v];
+                    one(ac[f], v, (woc * 16 + 4 * (lane >> 4) + v) * Geo::YPITCH +
+                                      (wpx * F + f) * 16 + (lane & 15));
         }
     };
+#pragma unroll
+    for (int g = 1; g < KG; ++g) {
+        if (g == 1 && kg == 0) put(0, acc, false);
+        __syncthreads();
+        if (kg == g) put(0, acc, true);
+    }
     // A non-finite sum may hold a product the reference skips: the block
-    // notes whether any of its sums is non-finite (a test of the
-    // accumulators, before they go through LDS) in one LDS word, and only a
-    // block that has one takes the epilogue that recomputes them; the others
-    // store as fast as they would without the test.
-    {
+    // notes whether any of its sums is non-finite (a test of the last
+    // group's registers, which hold the finished sums) in one LDS word, and
+    // only a block that has one takes the epilogue that recomputes them; the
+    // others store as fast as they would without the test.
+    if (kg == KG - 1) {
         bool bad = false;
 #pragma unroll
         for (int f = 0; f < F; ++f) bad |= !all_finite4(acc[f][0], acc[f][1], acc[f][2], acc[f][3]);
@@ -668,23 +783,25 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         }
         if (bad) smem[Geo::FLAG] = 1.f;
     }
-    put(0, acc);
-    if (WMODE == 3) {
+    if (KG == 1) {
+        put(0, acc, false);
+        if (WMODE == 3) {
 #pragma unroll
-        for (int ph = 1; ph < 4; ++ph) put(ph, acc3[ph > 0 ? ph - 1 : 0]);
+            for (int ph = 1; ph < 4; ++ph) put(ph, acc3[ph > 0 ? ph - 1 : 0], false);
+        }
     }
     __syncthreads();
     float *outb = a.out + (int64_t)n * a.out_img;
     const int np = p1 - p0;
     if (smem[Geo::FLAG] != 0.f) {
-        direct_fwd_epilogue_exact<KT, R, S, WMODE, EPI, PD>(a, ys, Geo::YPITCH, outb, n, p0, np,
-                                                            co0, wave, lane);
+        direct_fwd_epilogue_exact<KT, R, S, WMODE, EPI, PD, NW>(a, ys, Geo::YPITCH, outb, n, p0,
+                                                                np, co0, wave, lane);
         return;
     }
     if (EPI == 3) {
         // Element e of a channel's run: super-pixel p0 + e/2, column phase e&1;
         // consecutive lanes write consecutive pixels of a full-resolution row.
-        for (int row = wave; row < KT; row += 4) {
+        for (int row = wave; row < KT; row += NW) {
             const int co = co0 + row;
             if (co >= a.CO) break;
             float *dst = outb + (int64_t)co * a.fh * a.fw;
@@ -699,7 +816,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
                 }
         }
     } else if (EPI == 1) {
-        for (int row = wave; row < KT; row += 4) {
+        for (int row = wave; row < KT; row += NW) {
             const int co = co0 + row;
             if (co >= a.CO) break;
             const int c = co >> 2, py = (co >> 1) & 1, px = co & 1;
@@ -714,7 +831,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
         }
     } else if (a.out_vec) {
         const int n4 = np >> 2;
-        for (int row = wave; row < KT; row += 4) {
+        for (int row = wave; row < KT; row += NW) {
             const int co = co0 + row;
             if (co >= a.CO) break;
             float *dst = outb + (int64_t)co * a.OHW + p0;
@@ -725,7 +842,7 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
             }
         }
     } else {
-        for (int row = wave; row < KT; row += 4) {
+        for (int row = wave; row < KT; row += NW) {
             const int co = co0 + row;
             if (co >= a.CO) break;
             float *dst = outb + (int64_t)co * a.OHW + p0;
@@ -735,10 +852,23 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     }
 }
 
+// Waves per SIMD the forward kernel is compiled for: two blocks per CU, or
+// with wave groups as many as the block's LDS lets share a CU.
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int KG>
+constexpr int direct_fwd_waves_per_simd() {
+    return KG == 1 ? 2
+                   : KG * (2 * DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>::kBytes <=
+                                   160 * 1024
+                               ? 2
+                               : 1);
+}
+
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool WVEC, bool S2 = false, bool RF = false, int PD = 0>
-__global__ void __launch_bounds__(256, 2) direct_fwd_kernel(const DirectArgs a) {
-    direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WVEC, S2, RF, PD>(a, blockIdx.x,
+          bool WVEC, bool S2 = false, bool RF = false, int PD = 0, int KG = 1>
+__global__ void __launch_bounds__(
+    256 * KG, (direct_fwd_waves_per_simd<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>()))
+    direct_fwd_kernel(const DirectArgs a) {
+    direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WVEC, S2, RF, PD, KG>(a, blockIdx.x,
                                                                                gridDim.x);
 }
 

@@ -729,9 +729,9 @@ struct DirectFwdPlan {
 };
 
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, bool S2 = false,
-          bool RF = false, int PD = 0>
+          bool RF = false, int PD = 0, int KG = 1>
 bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>;
     if (P.R != R || P.S != S) return false;
     // Halo filter: the layer's, or for the phase form its G offsets.
     constexpr int HR = WMODE == 3 ? Dxs2Taps<R, S, PD>::DR : R;
@@ -823,20 +823,20 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
 }
 
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool S2 = false, bool RF = false, int PD = 0>
+          bool S2 = false, bool RF = false, int PD = 0, int KG = 1>
 int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
-    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE>;
+    using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>;
     int rc;
     if (pl.wvec) {
-        constexpr auto kern =
-            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, WMODE != 2, S2, RF, PD>;
+        constexpr auto kern = direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI,
+                                                WMODE != 2, S2, RF, PD, KG>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
-        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
+        kern<<<dim3((unsigned)pl.blocks), dim3(256 * KG), Geo::kBytes, st>>>(pl.a);
     } else {
         constexpr auto kern =
-            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, false, S2, RF, PD>;
+            direct_fwd_kernel<KT, F, CB, R, S, ROWS, PITCH, WMODE, EPI, false, S2, RF, PD, KG>;
         if ((rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return rc;
-        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(pl.a);
+        kern<<<dim3((unsigned)pl.blocks), dim3(256 * KG), Geo::kBytes, st>>>(pl.a);
     }
     return launch_status();
 }
@@ -844,12 +844,13 @@ int direct_fwd_run(const DirectFwdPlan &pl, hipStream_t st) {
 // Direct forward-shaped variants: block tile (KT output channels x F
 // fragments per wave), input-channel chunk, filter, halo rows and pitch.
 template <int KT_, int F_, int CB_, int R_, int S_, int ROWS_, int PITCH_, bool S2_ = false,
-          bool RF_ = false, int PD_ = 0>
+          bool RF_ = false, int PD_ = 0, int KG_ = 1>
 struct FwdVariant {
     static constexpr int KT = KT_, F = F_, CB = CB_, R = R_, S = S_, ROWS = ROWS_, PITCH = PITCH_;
     static constexpr bool S2 = S2_;  // stride-2 halo rows split by column parity
     static constexpr bool RF = RF_;  // one output row (<= 16 pixels) per fragment
     static constexpr int PD = PD_;   // phase form: the layer's padding
+    static constexpr int KG = KG_;   // forward launches: groups of four waves per block
 };
 // 3x3 stride 1 (forward and data gradient): 64 x 208-pixel tiles.
 #ifndef KATSU_FWDV
@@ -865,7 +866,7 @@ using FwdS2 = FwdVariant<KATSU_FWD_S2_VARIANT>;
 // 3x3 stride 2 forward on rows of at most 16 pixels: 64 channels x 7 rows,
 // one row per fragment.
 #ifndef KATSU_FWD_S2R_VARIANT
-#define KATSU_FWD_S2R_VARIANT 64, 7, 8, 3, 3, 16, 32, true, true
+#define KATSU_FWD_S2R_VARIANT 64, 7, 16, 3, 3, 16, 32, true, true, 0, 2
 #endif
 using FwdS2R = FwdVariant<KATSU_FWD_S2R_VARIANT>;
 // Stride-2 data gradient by super-pixels: a 4x4 super-filter (7x7 layers
@@ -885,15 +886,19 @@ using DxPh = FwdVariant<KATSU_DX_PH_VARIANT>;
 
 #define KATSU_FWD_VARIANT FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::PITCH
 
+// The variant's wave groups apply to forward launches (WMODE 0) only: the
+// stride-1 dX shares its kernel body with the one-launch backward, whose dX
+// blocks run four waves, and both must give the same bits.
 template <class V, int WMODE, int EPI>
 bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    constexpr int KG = WMODE == 0 ? V::KG : 1;
     DirectFwdPlan pl;
     if (P.CO < V::KT / 2 ||
         !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, V::S2, V::RF,
-                         V::PD>(P, &pl))
+                         V::PD, KG>(P, &pl))
         return false;
     *rc = direct_fwd_run<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE, EPI, V::S2,
-                         V::RF, V::PD>(pl, st);
+                         V::RF, V::PD, KG>(pl, st);
     return true;
 }
 

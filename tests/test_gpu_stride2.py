@@ -136,6 +136,7 @@ FWD_CASES = [
     ((64, 16, 28, 28), (128, 16, 3, 3)),  # 14-pixel rows, 7-row tiles
     ((64, 20, 27, 29), (100, 20, 3, 3)),  # 15-pixel rows; a partial channel block
     ((64, 22, 28, 30), (96, 22, 3, 3)),   # 22 channels: 4-byte weight loads
+    ((64, 40, 28, 28), (64, 40, 3, 3)),   # three 16-channel stages; 4-row tiles
 ]
 
 
