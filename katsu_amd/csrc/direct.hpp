@@ -152,6 +152,9 @@ struct DirectArgs {
     // WMODE 2 / EPI 1: the layer's C, R, S, padding, the super-filter's
     // offsets, C*R*S, and the full-resolution output size.
     int g_c, g_r, g_s, g_pad, g_amin, g_bmin, g_crs, fh, fw;
+    // BAND tiles (direct_bwd_band_kernel): tile t of an image starts at
+    // pixel t*band_px + band_off (plain tiles: t*tile_px).
+    int band_px, band_off;
 };
 
 // The (G offset, phase) pairs of the phase-form stride-2 data gradient of an
@@ -327,7 +330,7 @@ __device__ __forceinline__ void direct_fwd_epilogue_exact(const DirectArgs &a, c
 // back-to-back MFMAs.  The groups' sums are added in group order in the
 // epilogue's LDS transpose.
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int EPI,
-          bool WVEC, bool S2 = false, bool RF = false, int PD = 0, int KG = 1>
+          bool WVEC, bool S2 = false, bool RF = false, int PD = 0, int KG = 1, bool BAND = false>
 __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, int nb) {
     using Geo = DirectFwdGeo<KT, F, CB, R, S, ROWS, PITCH, WMODE, KG>;
     constexpr int RS = R * S;
@@ -355,7 +358,8 @@ __device__ __forceinline__ void direct_fwd_block(const DirectArgs &a, int bid, i
     const int cob = t % a.co_blocks;
     const int rest = t / a.co_blocks;
     const int n = rest / a.tiles_img;
-    const int p0 = (rest - n * a.tiles_img) * a.tile_px;
+    const int p0 = BAND ? (rest - n * a.tiles_img) * a.band_px + a.band_off
+                        : (rest - n * a.tiles_img) * a.tile_px;
     const int p1 = min(p0 + a.tile_px, a.OHW);
     const int oy0 = a.fd_ow.div(p0);
     const int iy0 = oy0 * a.st - a.pady;
@@ -1334,6 +1338,32 @@ __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
     else
         direct_fwd_block<XKT, XF, XCB, R, S, XROWS, XPITCH, XWMODE, XEPI, XWVEC, false, XRF, XPD>(
             dx, blockIdx.x - nbw, gridDim.x - nbw);
+}
+
+// The one-launch backward with the stride-1 dX tiles in two sizes: an
+// image's rows are cut into bands, and each band into a larger first tile
+// and a smaller second one.  Blocks [nbw, nbw + nx1) take the first tiles
+// (dx1, XF1 fragments per wave) and are dispatched beside the dW blocks at
+// the start; the rest take the second tiles (dx2, XF2), which the CU slots
+// pick up as the first ones retire.  A CU thus runs one dW block beside a
+// larger then a smaller dX block, and its two slots end closer together
+// than with two equal dX blocks, which outlast the dW block.  Tile shape
+// does not change any output's sum order, so dX has the bits of the
+// separate call.
+template <int XKT, int XF1, int XF2, int XCB, int R, int S, int XROWS, int XPITCH, bool XWVEC,
+          int KT, int CT, int ROWS, int PITCH, int GPC, int WKF, bool FULL>
+__global__ void __launch_bounds__(256, 2)
+    direct_bwd_band_kernel(const DirectArgs dx1, const DirectArgs dx2, const DirectDwArgs dw,
+                           int nbw, int nx1) {
+    const int b = blockIdx.x;
+    if (b < nbw)
+        direct_dw_block<KT, CT, R, S, ROWS, PITCH, GPC, WKF, FULL>(dw, b, nbw);
+    else if (b - nbw < nx1)
+        direct_fwd_block<XKT, XF1, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC, false, false, 0, 1,
+                         true>(dx1, b - nbw, nx1);
+    else
+        direct_fwd_block<XKT, XF2, XCB, R, S, XROWS, XPITCH, 1, 0, XWVEC, false, false, 0, 1,
+                         true>(dx2, b - nbw - nx1, (int)gridDim.x - nbw - nx1);
 }
 
 // dw[e] = beta*dw[e] + sum_s part[s][e].  Thread (e4, grp) sums splits

@@ -812,6 +812,7 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
         a.g_crs = (int)(P.g_c * P.g_r * P.g_s);
         a.fh = (int)P.fh;
         a.fw = (int)P.fw;
+        a.band_px = a.band_off = 0;
         // 16-byte weight loads: every float4 of a chunk row must lie inside
         // the row, which holds when rows start and end on multiples of 4.
         pl->wvec = WMODE != 2 && (WMODE == 0 ? P.CI % 4 == 0 : P.CO % 4 == 0) && aligned16(P.w);
@@ -1206,13 +1207,81 @@ int bwd_fused_dx(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st
                                              false, false>(xp, wp, st);
 }
 
-// The dX blocks of a shared launch: the stride-1 form (FwdV, WMODE 1) with a
-// stride-1 dW variant, the stride-2 phase form (DxPh, WMODE 3) with a
-// stride-2 one.
+// Banded stride-1 dX tiles for the shared launch (direct_bwd_band_kernel):
+// bands of two plain tiles' rows, each cut into a first tile of
+// ceil(rows/2) rows and a second of the rest, when the image is whole bands,
+// the tiles fit kBandF1 and kBandF2 fragments and the halo rows, and there
+// is one first-tile block per dW block (one per CU slot at the start).
+#ifndef KATSU_FUSED_BAND
+#define KATSU_FUSED_BAND 1
+#endif
+constexpr int kBandF1 = 14, kBandF2 = 11;
+
+bool band_plans(const DirectFwdPlan &xp, const DirectDwPlan &wp, DirectArgs *a1, DirectArgs *a2,
+                int64_t *n1, int64_t *n2) {
+    const DirectArgs &a = xp.a;
+    if (!KATSU_FUSED_BAND || a.st != 1) return false;
+    const int band_px = 2 * a.tile_px;
+    if (band_px % a.OW != 0) return false;
+    const int band_rows = band_px / a.OW;
+    const int r1 = (band_rows + 1) / 2, r2 = band_rows - r1;
+    if (r2 < 1 || a.OH % band_rows != 0 || r1 * a.OW > 16 * kBandF1 ||
+        r2 * a.OW > 16 * kBandF2 || r1 - 1 + FwdV::R > FwdV::ROWS)
+        return false;
+    const int bands = a.OH / band_rows;
+    const int64_t nb = (int64_t)a.co_blocks * a.N * bands;
+    if (nb != wp.blocks || 2 * nb != xp.blocks) return false;
+    *a1 = a;
+    *a2 = a;
+    a1->tiles_img = a2->tiles_img = bands;
+    a1->band_px = a2->band_px = band_px;
+    a1->tile_px = r1 * a.OW;
+    a1->band_off = 0;
+    a2->tile_px = r2 * a.OW;
+    a2->band_off = r1 * a.OW;
+    const bool v4 = band_px % 4 == 0 && (r1 * a.OW) % 4 == 0 && a.OHW % 4 == 0;
+    a1->out_vec = a2->out_vec = a.out_vec && v4 ? 1 : 0;
+    *n1 = *n2 = nb;
+    return true;
+}
+
+template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL,
+          bool XWVEC>
+int bwd_band_kernel_launch(const DirectArgs &a1, const DirectArgs &a2, int64_t n1, int64_t n2,
+                           const DirectDwPlan &wp, hipStream_t st) {
+    using XGeo = DirectFwdGeo<FwdV::KT, kBandF1, FwdV::CB, R, S, FwdV::ROWS, FwdV::PITCH, 1>;
+    constexpr auto kern =
+        direct_bwd_band_kernel<FwdV::KT, kBandF1, kBandF2, FwdV::CB, R, S, FwdV::ROWS,
+                               FwdV::PITCH, XWVEC, KT, CT, ROWS, PITCH, GPC, WKF, FULL>;
+    const int rc = lds_optin<kern>(kLdsMax);
+    if (rc != KATSU_OK) return rc;
+    const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
+    kern<<<dim3((unsigned)(wp.blocks + n1 + n2)), dim3(256), lds, st>>>(a1, a2, wp.a,
+                                                                      (int)wp.blocks, (int)n1);
+    return launch_status();
+}
+
+// The dX blocks of a shared launch: the stride-1 form (FwdV, WMODE 1, banded
+// when band_plans applies) with a stride-1 dW variant, the stride-2 phase
+// form (DxPh, WMODE 3) with a stride-2 one.
 template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
 int bwd_fused_variant(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
-    if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S)
+    if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S) {
+        DirectArgs a1, a2;
+        int64_t n1, n2;
+        if (band_plans(xp, wp, &a1, &a2, &n1, &n2)) {
+            if (wp.full)
+                return xp.wvec ? bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
+                                                        true>(a1, a2, n1, n2, wp, st)
+                               : bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
+                                                        false>(a1, a2, n1, n2, wp, st);
+            return xp.wvec ? bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
+                                                    true>(a1, a2, n1, n2, wp, st)
+                           : bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
+                                                    false>(a1, a2, n1, n2, wp, st);
+        }
         return bwd_fused_dx<FwdV, 1, 0, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
+    }
     else if constexpr (ST == 2 && R == DxPh::R && S == DxPh::S)
         return bwd_fused_dx<DxPh, 3, 3, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
     return KATSU_E_INVALID;

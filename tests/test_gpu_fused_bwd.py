@@ -83,6 +83,33 @@ def test_fused_matches_separate(xs, ws, st, p, fused, dev):
             f"dW beta={beta}: worst excess {(err - lim_b).max().item():.3e}"
 
 
+@pytest.mark.parametrize("xs,ws,st,p", [((32, 64, 56, 56), (64, 64, 3, 3), 1, 1),
+                                        ((32, 128, 28, 28), (256, 128, 3, 3), 2, 1)])
+def test_fused_matches_separate_nonfinite(xs, ws, st, p, dev):
+    """Inf, -Inf and NaN planted in G and w (border and interior): the shared
+    launch's dX blocks (at config 3 the two-size tiles of the shared launch,
+    at config 4a the phase form) take the recompute of non-finite outputs as
+    the separate dX call does, so the two dX tensors hold the same bits,
+    NaNs included; dW's non-finite classes agree too."""
+    import torch
+
+    from katsu_amd import ops
+    x, w, g = _tensors(xs, ws, st, p, dev)
+    n, k, oh, ow = g.shape
+    g[0, 0, 0, 0] = float("inf")
+    g[n // 2, k // 3, oh // 2, ow - 1] = float("-inf")
+    g[n - 1, k - 1, oh - 1, ow // 3] = float("nan")
+    w[1, 2, 0, 1] = float("inf")
+    dx_s = ops.conv2d_backward_data(g, w, x.shape, st, p)
+    dw_s = ops.conv2d_backward_filter(x, g, w.shape, st, p)
+    dx_f, dw_f = ops.conv2d_backward(x, w, g, st, p)
+    torch.cuda.synchronize()
+    assert not torch.isfinite(dx_s).all(), "the planted values must reach dX"
+    assert torch.equal(dx_f.view(torch.int32), dx_s.view(torch.int32)), "dX bits"
+    for f in (torch.isnan, torch.isposinf, torch.isneginf):
+        assert torch.equal(f(dw_f), f(dw_s)), f"dW {f.__name__}"
+
+
 def test_fused_caller_workspace_and_graph_replay(dev):
     import torch
 
