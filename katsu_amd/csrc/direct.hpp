@@ -1340,6 +1340,24 @@ __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
             dx, blockIdx.x - nbw, gridDim.x - nbw);
 }
 
+// The forward with tiles of two fragment counts: an image's first tiles have
+// F fragments, the rest F-1, laid out with BAND offsets (a1: the F tiles,
+// a2: the others).  The F tiles are the grid's first n1 blocks, which the
+// dispatcher hands out one per CU before any CU takes a second block, so no
+// CU holds two of them: a CU's two blocks then hold at most 2F-1 fragment
+// columns, where equal tiles of F fragments (of which the image's pixels
+// fill F-1/4 on average) hold 2F.
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, bool WVEC>
+__global__ void __launch_bounds__(256, 2)
+    direct_fwd_mix_kernel(const DirectArgs a1, const DirectArgs a2, int n1) {
+    if ((int)blockIdx.x < n1)
+        direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, 0, 0, WVEC, false, false, 0, 1, true>(
+            a1, blockIdx.x, n1);
+    else
+        direct_fwd_block<KT, F - 1, CB, R, S, ROWS, PITCH, 0, 0, WVEC, false, false, 0, 1, true>(
+            a2, blockIdx.x - n1, (int)gridDim.x - n1);
+}
+
 // The one-launch backward with the stride-1 dX tiles in two sizes: an
 // image's rows are cut into bands, and each band into a larger first tile
 // and a smaller second one.  Blocks [nbw, nbw + nx1) take the first tiles

@@ -903,9 +903,57 @@ bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     return true;
 }
 
+// The stride-1 forward with tiles of F and F-1 fragments (direct_fwd_mix_kernel)
+// when the plain plan's tiles are whole fragments short of F: an image's
+// ceil(OHW/16) fragments over its tiles_img tiles, the first ones F, the
+// rest F-1, with the F tiles fewer than one per CU slot of the grid's
+// first half.  False = not applicable (the plain launch runs).
+#ifndef KATSU_FWD_MIX
+#define KATSU_FWD_MIX 1
+#endif
+bool try_direct_mix(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    using V = FwdV;
+    DirectFwdPlan pl;
+    if (!KATSU_FWD_MIX || P.CO < V::KT / 2 ||
+        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, 0>(P, &pl))
+        return false;
+    const DirectArgs &a = pl.a;
+    if (a.OHW % 16 != 0 || a.tiles_img < 2) return false;
+    const int64_t q = a.OHW / 16, T = a.tiles_img;
+    const int64_t fs = q / T, nbig = q - fs * T;
+    if (fs + 1 != V::F || nbig == 0) return false;
+    const int64_t n1 = (int64_t)a.co_blocks * a.N * nbig, n2 = pl.blocks - n1;
+    if (2 * n1 > pl.blocks || n2 != (int64_t)a.co_blocks * a.N * (T - nbig)) return false;
+    // Halo rows of the larger tile (whole fragments, any start column).
+    if ((tile_row_span(16 * V::F, a.OW, a.OH) - 1) * a.st + V::R > V::ROWS) return false;
+    DirectArgs a1 = a, a2 = a;
+    a1.tile_px = a1.band_px = 16 * V::F;
+    a1.tiles_img = (int)nbig;
+    a1.band_off = 0;
+    a2.tile_px = a2.band_px = 16 * (V::F - 1);
+    a2.tiles_img = (int)(T - nbig);
+    a2.band_off = (int)(16 * V::F * nbig);
+    a1.out_vec = a2.out_vec = (a.OHW % 4 == 0 && aligned16(P.out)) ? 1 : 0;
+    using Geo = DirectFwdGeo<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, 0>;
+    if (pl.wvec) {
+        constexpr auto kern =
+            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, true>;
+        if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
+        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a1, a2, (int)n1);
+    } else {
+        constexpr auto kern =
+            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, false>;
+        if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
+        kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a1, a2, (int)n1);
+    }
+    *rc = launch_status();
+    return true;
+}
+
 // Forward-shaped direct launch; false = no variant applies.
 template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    if (WMODE == 0 && P.st == 1 && P.CO >= FwdV::KT && try_direct_mix(P, st, rc)) return true;
     if (P.st == 1 && P.CO >= FwdV::KT) return try_direct<FwdV, WMODE, 0>(P, st, rc);
     if (WMODE == 0 && P.st == 2) {
         if (P.OW <= 16 && try_direct<FwdS2R, 0, 0>(P, st, rc)) return true;

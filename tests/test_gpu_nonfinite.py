@@ -148,3 +148,30 @@ def test_nonfinite_host_entry_points(dev):
     _check(y, y_ref, ys, 64 * 9, "host fwd")
     _check(dx, dx_ref, dxs, 64 * 9, "host dX")
     _check(dw, dw_ref, dws, 9 * 56 * 56, "host dW")
+
+
+@pytest.mark.parametrize("plant", [False, True])
+def test_forward_two_fragment_counts(plant, dev):
+    """Config 3's forward at N = 16, the smallest batch that takes the tiles
+    of two fragment counts (each image's first tiles 13 fragments, the rest
+    12): every output against the oracle, on finite data and with Inf and NaN
+    planted in x and w (the classes exactly, finite values within the f32
+    bound)."""
+    import torch
+
+    from katsu_amd import ops
+    c = dict(synth.CONV_CONFIGS["c3_resnet"])
+    c["x"] = (16,) + c["x"][1:]
+    if plant:
+        x, w, _ = _plant(c)
+    else:
+        x, w = synth.conv_inputs(c)
+    st, p = c["stride"], c["pad"]
+    print(f"\nc3_resnet N=16 forward plant={plant}", flush=True)
+    y = ops.conv2d_forward(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), st, p)
+    torch.cuda.synchronize()
+    y_ref = O.conv2d_forward(x, w, st, p)
+    ys = O.conv2d_forward(_finite0(x), _finite0(w), st, p)
+    if plant:
+        assert np.isfinite(y_ref).any() and not np.isfinite(y_ref).all()
+    _check(y.cpu().numpy(), y_ref, ys, w.shape[1] * w.shape[2] * w.shape[3], "fwd N=16")
