@@ -60,7 +60,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(synth.CONV_CONFIGS))
     ap.add_argument("--configs", nargs="+", default=["all"],
                     help="other conv workloads measured beside the headline "
@@ -89,13 +89,14 @@ def capture(fn):
     return g
 
 
-def timed_steps(step, k, reset=None):
+def timed_steps(step, k, reset=None, warm=0):
     """Captures `step` STEPS_PER_GRAPH times over in one HIP graph (and the
     remainder of k in a second) and returns the milliseconds that replaying
     exactly k steps takes, and the per-step milliseconds of each full replay
     (events between replays).  Several steps per graph keep the per-replay
     launch cost of a HIP graph out of the per-step time, as a training loop
-    captured whole would.  `reset` runs after the untimed first replay and
+    captured whole would.  Untimed replays of the same graph first run at
+    least `warm` steps (one replay at least).  `reset` runs after them and
     before the timed ones (the caller poisons the outputs there, so a check
     afterwards shows that the timed replays wrote them)."""
     import torch
@@ -103,7 +104,8 @@ def timed_steps(step, k, reset=None):
     full, rem = divmod(k, per)
     g_full = capture(lambda: [step() for _ in range(per)])
     g_rem = capture(lambda: [step() for _ in range(rem)]) if rem else None
-    g_full.replay()
+    for _ in range(max(1, -(-warm // per))):
+        g_full.replay()
     torch.cuda.synchronize()
     if reset is not None:
         reset()
@@ -262,8 +264,12 @@ def measure_conv(name, args, dev, poison=True):
         fwd()
         bwd()
 
-    for _ in range(args.warmup):
-        step()
+    # One eager step (the reference outputs for the check below, and the
+    # library's plans); the W warmup steps then run as replays of the timed
+    # step's own graph, back to back: the GPU's clock settles under dense
+    # work (about 10 ms of it), which eager steps, with the host's launch
+    # gaps between them, do not give it.
+    step()
     torch.cuda.synchronize()
     eager = (yd.clone(), dxd.clone(), dwd.clone())
 
@@ -271,7 +277,8 @@ def measure_conv(name, args, dev, poison=True):
         for t in (yd, dxd, dwd):
             t.fill_(float("nan"))
 
-    total_ms, spread = timed_steps(step, args.steps, reset=reset if poison else None)
+    total_ms, spread = timed_steps(step, args.steps, reset=reset if poison else None,
+                                   warm=args.warmup)
     ms_per_step = total_ms / args.steps
     step_med, step_iqr = med_iqr(spread)
     # The outputs were NaN when the timed replays began: the replays wrote
@@ -525,7 +532,8 @@ def measure_matmul(n, args, dev):
     mstep()
     torch.cuda.synchronize()
     reps = max(1, args.matmul_steps if n >= 2048 else 10 * args.matmul_steps)
-    mms = timed_steps(mstep, reps)[0] / reps
+    # The W warmup steps as graph replays (at 4096 a few: each is 3 ms).
+    mms = timed_steps(mstep, reps, warm=args.warmup if n < 2048 else 5)[0] / reps
     flops = 2 * n ** 3
     nbytes = 4 * n * n
     kern = {"fwd": time_pass(fwd, reps, 1, flops, 3 * nbytes),
