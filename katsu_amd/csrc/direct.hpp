@@ -1358,9 +1358,9 @@ __global__ void __launch_bounds__(256, 2)
             a2, blockIdx.x - n1, (int)gridDim.x - n1);
 }
 
-// The one-launch backward with the stride-1 dX tiles in two sizes: an
-// image's rows are cut into bands, and each band into a larger first tile
-// and a smaller second one.  Blocks [nbw, nbw + nx1) take the first tiles
+// The one-launch backward with the stride-1 dX tiles in two sizes: each
+// image holds as many larger first tiles as smaller second ones (BAND
+// offsets place each set).  Blocks [nbw, nbw + nx1) take the first tiles
 // (dx1, XF1 fragments per wave) and are dispatched beside the dW blocks at
 // the start; the rest take the second tiles (dx2, XF2), which the CU slots
 // pick up as the first ones retire.  A CU thus runs one dW block beside a

@@ -1255,9 +1255,9 @@ int bwd_fused_dx(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st
                                              false, false>(xp, wp, st);
 }
 
-// Banded stride-1 dX tiles for the shared launch (direct_bwd_band_kernel):
-// bands of two plain tiles' rows, each cut into a first tile of
-// ceil(rows/2) rows and a second of the rest, when the image is whole bands,
+// Two-size stride-1 dX tiles for the shared launch (direct_bwd_band_kernel):
+// per band of two plain tiles' rows, a first tile of ceil(rows/2) rows and a
+// second of the rest, when the image is whole bands,
 // the tiles fit kBandF1 and kBandF2 fragments and the halo rows, and there
 // is one first-tile block per dW block (one per CU slot at the start).
 #ifndef KATSU_FUSED_BAND
@@ -1279,15 +1279,17 @@ bool band_plans(const DirectFwdPlan &xp, const DirectDwPlan &wp, DirectArgs *a1,
     const int bands = a.OH / band_rows;
     const int64_t nb = (int64_t)a.co_blocks * a.N * bands;
     if (nb != wp.blocks || 2 * nb != xp.blocks) return false;
+    // The first tiles lie together at the top of the image and the second
+    // ones below them, so each set's neighbouring tiles share their halo
+    // rows while they run at the same time (one fetch into L2).
     *a1 = a;
     *a2 = a;
     a1->tiles_img = a2->tiles_img = bands;
-    a1->band_px = a2->band_px = band_px;
-    a1->tile_px = r1 * a.OW;
+    a1->tile_px = a1->band_px = r1 * a.OW;
     a1->band_off = 0;
-    a2->tile_px = r2 * a.OW;
-    a2->band_off = r1 * a.OW;
-    const bool v4 = band_px % 4 == 0 && (r1 * a.OW) % 4 == 0 && a.OHW % 4 == 0;
+    a2->tile_px = a2->band_px = r2 * a.OW;
+    a2->band_off = bands * r1 * a.OW;
+    const bool v4 = (r1 * a.OW) % 4 == 0 && (r2 * a.OW) % 4 == 0 && a.OHW % 4 == 0;
     a1->out_vec = a2->out_vec = a.out_vec && v4 ? 1 : 0;
     *n1 = *n2 = nb;
     return true;
