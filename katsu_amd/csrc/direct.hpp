@@ -209,9 +209,15 @@ struct Dxs2Taps {
 template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, int WMODE, int KG = 1>
 struct DirectFwdGeo {
     static constexpr int RS = R * S;
-    static_assert(PITCH == 32 || PITCH % 64 == 0, "halo row pitch: 32 or a multiple of 64");
+    // Halo rows: 32 floats (staged in pairs), or PITCH >= 64 floats of which
+    // the first HCOLS are staged (whole 64-float loads; the rest of a row is
+    // never read).  A pitch congruent to the output row length mod 16 keeps a
+    // 16-pixel fragment that runs from one row's end into the next on 16
+    // distinct address residues mod 16, as a fragment inside one row is.
+    static_assert(PITCH == 32 || (PITCH >= 64 && PITCH % 8 == 0), "halo row pitch");
     static_assert(PITCH != 32 || ROWS % 2 == 0, "32-float rows are staged in pairs");
-    static constexpr int CPITCH = ROWS * PITCH + 16;    // channel pitch, == 16 (mod 32)
+    static constexpr int HCOLS = PITCH >= 64 ? PITCH / 64 * 64 : PITCH;
+    static constexpr int CPITCH = (ROWS * PITCH + 31) / 32 * 32 + 16;  // == 16 (mod 32)
     static constexpr int XS = CB * CPITCH;              // input tile
     // Weight tile, kept in the global order of its rows:
     //   WMODE 0, 2: KT rows (co) of CB*RS floats, pitch CB*RS + 4

@@ -743,7 +743,7 @@ bool direct_fwd_plan(const DirectFwdProblem &P, DirectFwdPlan *pl) {
     constexpr int WPX = 4 / (KT / 16);
     const int64_t OHW = P.OH * P.OW;
     const int64_t ncols = (P.OW - 1) * P.st + HS;
-    if (ncols > PITCH) return false;
+    if (ncols > Geo::HCOLS) return false;
     // Buffer resources address one image of `in` and all of `w` in bytes.
     const int64_t in_img = P.CI * P.H * P.W;
     const int64_t w_elems = WMODE == 2 ? P.CI * P.g_c * P.g_r * P.g_s : P.CO * P.CI * R * S;
@@ -858,6 +858,16 @@ struct FwdVariant {
 #define KATSU_FWDV 64, 13, 8, 3, 3, 7, 64
 #endif
 using FwdV = FwdVariant<KATSU_FWDV>;
+// The same tile with halo rows 8 floats longer, for output rows of 8 (mod
+// 16) pixels (56 at config 3): a fragment that runs from one row's end into
+// the next then reads 16 distinct LDS banks, as a fragment inside a row
+// does, instead of meeting the other channel group of its half-wave on the
+// same banks.  The loads and the sums are those of FwdV, so are the bits.
+#ifndef KATSU_FWD_PITCH8
+#define KATSU_FWD_PITCH8 1
+#endif
+using FwdVP = FwdVariant<FwdV::KT, FwdV::F, FwdV::CB, FwdV::R, FwdV::S, FwdV::ROWS, FwdV::PITCH + 8>;
+inline bool fwd_pitch8(int64_t ow) { return KATSU_FWD_PITCH8 && ow % 16 == 8; }
 // 3x3 stride 2 forward: 64 x 64-pixel tiles, 32-float halo rows split by
 // column parity.
 #ifndef KATSU_FWD_S2_VARIANT
@@ -911,8 +921,8 @@ bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
 #ifndef KATSU_FWD_MIX
 #define KATSU_FWD_MIX 1
 #endif
+template <class V>
 bool try_direct_mix(const DirectFwdProblem &P, hipStream_t st, int *rc) {
-    using V = FwdV;
     DirectFwdPlan pl;
     if (!KATSU_FWD_MIX || P.CO < V::KT / 2 ||
         !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, 0>(P, &pl))
@@ -953,8 +963,13 @@ bool try_direct_mix(const DirectFwdProblem &P, hipStream_t st, int *rc) {
 // Forward-shaped direct launch; false = no variant applies.
 template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
-    if (WMODE == 0 && P.st == 1 && P.CO >= FwdV::KT && try_direct_mix(P, st, rc)) return true;
-    if (P.st == 1 && P.CO >= FwdV::KT) return try_direct<FwdV, WMODE, 0>(P, st, rc);
+    if (P.st == 1 && P.CO >= FwdV::KT) {
+        const bool p8 = fwd_pitch8(P.OW);
+        if (WMODE == 0 &&
+            (p8 ? try_direct_mix<FwdVP>(P, st, rc) : try_direct_mix<FwdV>(P, st, rc)))
+            return true;
+        return p8 ? try_direct<FwdVP, WMODE, 0>(P, st, rc) : try_direct<FwdV, WMODE, 0>(P, st, rc);
+    }
     if (WMODE == 0 && P.st == 2) {
         if (P.OW <= 16 && try_direct<FwdS2R, 0, 0>(P, st, rc)) return true;
         return try_direct<FwdS2, 0, 0>(P, st, rc);
@@ -1295,14 +1310,14 @@ bool band_plans(const DirectFwdPlan &xp, const DirectDwPlan &wp, DirectArgs *a1,
     return true;
 }
 
-template <int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF, bool FULL,
-          bool XWVEC>
+template <class XV, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF,
+          bool FULL, bool XWVEC>
 int bwd_band_kernel_launch(const DirectArgs &a1, const DirectArgs &a2, int64_t n1, int64_t n2,
                            const DirectDwPlan &wp, hipStream_t st) {
-    using XGeo = DirectFwdGeo<FwdV::KT, kBandF1, FwdV::CB, R, S, FwdV::ROWS, FwdV::PITCH, 1>;
+    using XGeo = DirectFwdGeo<XV::KT, kBandF1, XV::CB, R, S, XV::ROWS, XV::PITCH, 1>;
     constexpr auto kern =
-        direct_bwd_band_kernel<FwdV::KT, kBandF1, kBandF2, FwdV::CB, R, S, FwdV::ROWS,
-                               FwdV::PITCH, XWVEC, KT, CT, ROWS, PITCH, GPC, WKF, FULL>;
+        direct_bwd_band_kernel<XV::KT, kBandF1, kBandF2, XV::CB, R, S, XV::ROWS, XV::PITCH,
+                               XWVEC, KT, CT, ROWS, PITCH, GPC, WKF, FULL>;
     const int rc = lds_optin<kern>(kLdsMax);
     if (rc != KATSU_OK) return rc;
     const size_t lds = std::max(XGeo::kBytes, wp.lds_bytes);
@@ -1311,26 +1326,35 @@ int bwd_band_kernel_launch(const DirectArgs &a1, const DirectArgs &a2, int64_t n
     return launch_status();
 }
 
-// The dX blocks of a shared launch: the stride-1 form (FwdV, WMODE 1, banded
-// when band_plans applies) with a stride-1 dW variant, the stride-2 phase
-// form (DxPh, WMODE 3) with a stride-2 one.
+// The stride-1 dX blocks of a shared launch, FwdV's tile at XV's halo pitch:
+// two-size tiles when band_plans applies, else the plain tiles.
+template <class XV, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
+int bwd_fused_s1(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
+    DirectArgs a1, a2;
+    int64_t n1, n2;
+    if (band_plans(xp, wp, &a1, &a2, &n1, &n2)) {
+        if (wp.full)
+            return xp.wvec ? bwd_band_kernel_launch<XV, KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
+                                                    true>(a1, a2, n1, n2, wp, st)
+                           : bwd_band_kernel_launch<XV, KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
+                                                    false>(a1, a2, n1, n2, wp, st);
+        return xp.wvec ? bwd_band_kernel_launch<XV, KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
+                                                true>(a1, a2, n1, n2, wp, st)
+                       : bwd_band_kernel_launch<XV, KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
+                                                false>(a1, a2, n1, n2, wp, st);
+    }
+    return bwd_fused_dx<XV, 1, 0, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
+}
+
+// The dX blocks of a shared launch: the stride-1 form (FwdV or FwdVP, WMODE
+// 1) with a stride-1 dW variant, the stride-2 phase form (DxPh, WMODE 3)
+// with a stride-2 one.
 template <int ST, int KT, int CT, int R, int S, int ROWS, int PITCH, int GPC, int WKF>
 int bwd_fused_variant(const DirectFwdPlan &xp, const DirectDwPlan &wp, hipStream_t st) {
     if constexpr (ST != 2 && R == FwdV::R && S == FwdV::S) {
-        DirectArgs a1, a2;
-        int64_t n1, n2;
-        if (band_plans(xp, wp, &a1, &a2, &n1, &n2)) {
-            if (wp.full)
-                return xp.wvec ? bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
-                                                        true>(a1, a2, n1, n2, wp, st)
-                               : bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, true,
-                                                        false>(a1, a2, n1, n2, wp, st);
-            return xp.wvec ? bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
-                                                    true>(a1, a2, n1, n2, wp, st)
-                           : bwd_band_kernel_launch<KT, CT, R, S, ROWS, PITCH, GPC, WKF, false,
-                                                    false>(a1, a2, n1, n2, wp, st);
-        }
-        return bwd_fused_dx<FwdV, 1, 0, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
+        return fwd_pitch8(xp.a.OW)
+                   ? bwd_fused_s1<FwdVP, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st)
+                   : bwd_fused_s1<FwdV, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);
     }
     else if constexpr (ST == 2 && R == DxPh::R && S == DxPh::S)
         return bwd_fused_dx<DxPh, 3, 3, KT, CT, R, S, ROWS, PITCH, GPC, WKF>(xp, wp, st);

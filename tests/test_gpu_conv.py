@@ -168,8 +168,15 @@ def test_baseline_layers_small_batch(name, batch, dev):
     _check_full(x, w, g, c["stride"], c["pad"], dev, name)
 
 
+# A stride-1 3x3 layer with 40-pixel rows: like config 3's 56, 8 (mod 16), so
+# the direct kernels stage its halo rows 8 floats longer; 40 rows take the
+# plain (one tile size) forward tiles where config 3 takes two sizes.
+_ROWS40 = dict(x=(32, 64, 40, 40), w=(64, 64, 3, 3), stride=1, pad=1, law="u11")
+
+
 @pytest.mark.parametrize("name,batch", [("c3_resnet", 9), ("c4a_down3x3", 16),
-                                        ("c5_stem", 9), ("c4b_down1x1", 32)])
+                                        ("c5_stem", 9), ("c4b_down1x1", 32),
+                                        ("rows40", 32)])
 def test_production_kernels_full_parity(name, batch, dev):
     """The kernels the BASELINE configurations run (the direct 3x3 kernels of
     configs 3 and 4a and their one-launch backward, the stem's kernels, the
@@ -179,7 +186,7 @@ def test_production_kernels_full_parity(name, batch, dev):
     import torch
 
     from katsu_amd import ops
-    c = dict(synth.CONV_CONFIGS[name])
+    c = dict(_ROWS40 if name == "rows40" else synth.CONV_CONFIGS[name])
     c["x"] = (batch,) + c["x"][1:]
     x, w = synth.conv_inputs(c)
     g = synth.normal(synth.SEED_G, synth.out_shape(c))
