@@ -1353,15 +1353,18 @@ __global__ void __launch_bounds__(256, 2) direct_bwd_kernel(const DirectArgs dx,
 // CU holds two of them: a CU's two blocks then hold at most 2F-1 fragment
 // columns, where equal tiles of F fragments (of which the image's pixels
 // fill F-1/4 on average) hold 2F.
-template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, bool WVEC>
+// WMODE 1: the stride-1 dX (the same kernel on G with the flipped filter);
+// tile shape does not change any output's sum order, so dX has the bits of
+// the plain tiles and of the one-launch backward.
+template <int KT, int F, int CB, int R, int S, int ROWS, int PITCH, bool WVEC, int WMODE = 0>
 __global__ void __launch_bounds__(256, 2)
     direct_fwd_mix_kernel(const DirectArgs a1, const DirectArgs a2, int n1) {
     if ((int)blockIdx.x < n1)
-        direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, 0, 0, WVEC, false, false, 0, 1, true>(
+        direct_fwd_block<KT, F, CB, R, S, ROWS, PITCH, WMODE, 0, WVEC, false, false, 0, 1, true>(
             a1, blockIdx.x, n1);
     else
-        direct_fwd_block<KT, F - 1, CB, R, S, ROWS, PITCH, 0, 0, WVEC, false, false, 0, 1, true>(
-            a2, blockIdx.x - n1, (int)gridDim.x - n1);
+        direct_fwd_block<KT, F - 1, CB, R, S, ROWS, PITCH, WMODE, 0, WVEC, false, false, 0, 1,
+                         true>(a2, blockIdx.x - n1, (int)gridDim.x - n1);
 }
 
 // The one-launch backward with the stride-1 dX tiles in two sizes: each

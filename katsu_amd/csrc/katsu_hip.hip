@@ -913,19 +913,21 @@ bool try_direct(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     return true;
 }
 
-// The stride-1 forward with tiles of F and F-1 fragments (direct_fwd_mix_kernel)
-// when the plain plan's tiles are whole fragments short of F: an image's
-// ceil(OHW/16) fragments over its tiles_img tiles, the first ones F, the
-// rest F-1, with the F tiles fewer than one per CU slot of the grid's
-// first half.  False = not applicable (the plain launch runs).
+// The stride-1 forward (WMODE 0) or dX (WMODE 1) with tiles of F and F-1
+// fragments (direct_fwd_mix_kernel) when the plain plan's tiles are whole
+// fragments short of F: an image's ceil(OHW/16) fragments over its
+// tiles_img tiles, the first ones F, the rest F-1, with the F tiles fewer
+// than one per CU slot of the grid's first half.  False = not applicable
+// (the plain launch runs).
 #ifndef KATSU_FWD_MIX
 #define KATSU_FWD_MIX 1
 #endif
-template <class V>
+template <class V, int WMODE>
 bool try_direct_mix(const DirectFwdProblem &P, hipStream_t st, int *rc) {
+    static_assert(WMODE == 0 || WMODE == 1, "stride-1 forward and dX");
     DirectFwdPlan pl;
     if (!KATSU_FWD_MIX || P.CO < V::KT / 2 ||
-        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, 0>(P, &pl))
+        !direct_fwd_plan<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE>(P, &pl))
         return false;
     const DirectArgs &a = pl.a;
     if (a.OHW % 16 != 0 || a.tiles_img < 2) return false;
@@ -944,15 +946,15 @@ bool try_direct_mix(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     a2.tiles_img = (int)(T - nbig);
     a2.band_off = (int)(16 * V::F * nbig);
     a1.out_vec = a2.out_vec = (a.OHW % 4 == 0 && aligned16(P.out)) ? 1 : 0;
-    using Geo = DirectFwdGeo<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, 0>;
+    using Geo = DirectFwdGeo<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, WMODE>;
     if (pl.wvec) {
         constexpr auto kern =
-            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, true>;
+            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, true, WMODE>;
         if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a1, a2, (int)n1);
     } else {
         constexpr auto kern =
-            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, false>;
+            direct_fwd_mix_kernel<V::KT, V::F, V::CB, V::R, V::S, V::ROWS, V::PITCH, false, WMODE>;
         if ((*rc = lds_optin<kern>(Geo::kBytes)) != KATSU_OK) return true;
         kern<<<dim3((unsigned)pl.blocks), dim3(256), Geo::kBytes, st>>>(a1, a2, (int)n1);
     }
@@ -965,9 +967,9 @@ template <int WMODE>
 bool direct_fwd(const DirectFwdProblem &P, hipStream_t st, int *rc) {
     if (P.st == 1 && P.CO >= FwdV::KT) {
         const bool p8 = fwd_pitch8(P.OW);
-        if (WMODE == 0 &&
-            (p8 ? try_direct_mix<FwdVP>(P, st, rc) : try_direct_mix<FwdV>(P, st, rc)))
-            return true;
+        if constexpr (WMODE <= 1)
+            if (p8 ? try_direct_mix<FwdVP, WMODE>(P, st, rc) : try_direct_mix<FwdV, WMODE>(P, st, rc))
+                return true;
         return p8 ? try_direct<FwdVP, WMODE, 0>(P, st, rc) : try_direct<FwdV, WMODE, 0>(P, st, rc);
     }
     if (WMODE == 0 && P.st == 2) {
