@@ -175,3 +175,32 @@ def test_forward_two_fragment_counts(plant, dev):
     if plant:
         assert np.isfinite(y_ref).any() and not np.isfinite(y_ref).all()
     _check(y.cpu().numpy(), y_ref, ys, w.shape[1] * w.shape[2] * w.shape[3], "fwd N=16")
+
+
+@pytest.mark.parametrize("plant", [False, True])
+def test_dx_two_fragment_counts(plant, dev):
+    """The separate data-gradient call at config 3's shapes and N = 16, which
+    takes the same tiles of two fragment counts as the forward (the stride-1
+    dX is the forward's kernel on G with the flipped filter): every element
+    of dX against the oracle, on finite data and with Inf and NaN planted in
+    w and G."""
+    import torch
+
+    from katsu_amd import ops
+    c = dict(synth.CONV_CONFIGS["c3_resnet"])
+    c["x"] = (16,) + c["x"][1:]
+    if plant:
+        x, w, g = _plant(c)
+    else:
+        x, w = synth.conv_inputs(c)
+        g = synth.normal(synth.SEED_G, synth.out_shape(c))
+    st, p = c["stride"], c["pad"]
+    print(f"\nc3_resnet N=16 dX plant={plant}", flush=True)
+    dx = ops.conv2d_backward_data(torch.from_numpy(g).to(dev), torch.from_numpy(w).to(dev),
+                                  x.shape, st, p)
+    torch.cuda.synchronize()
+    dx_ref, _ = O.conv2d_backward(x, w, g, st, p)
+    dxs, _ = O.conv2d_backward(_finite0(x), _finite0(w), _finite0(g), st, p)
+    if plant:
+        assert np.isfinite(dx_ref).any() and not np.isfinite(dx_ref).all()
+    _check(dx.cpu().numpy(), dx_ref, dxs, w.shape[0] * w.shape[2] * w.shape[3], "dX N=16")
